@@ -153,6 +153,165 @@ size_t mfx_sdpa_workspace_size(const mfx_sdpa_args* args);
  * string ("flash_bf16_d128", "decode_splitkv", ...), or NULL if invalid. */
 const char* mfx_sdpa_kernel_name(const mfx_sdpa_args* args);
 
+/* ==========================================================================
+ * Generic ops: the graph regions the pattern matcher does not fuse.
+ * The reference evaluates these op by op with MLX (reference
+ * src/jax_mlx_pjrt.cpp:4396-4666, 4808-5009, 5298-5341, 5455-5560,
+ * 5738-5747); here a run of elementwise / broadcast / transpose / convert /
+ * select / compare / iota ops becomes one fused loop kernel.
+ * ========================================================================== */
+
+/* Element types of the generic ops (the three float codes above, plus): */
+enum {
+  MFX_I32 = 3,
+  MFX_PRED = 4, /* one byte, 0 or 1 */
+  MFX_I64 = 5,
+  MFX_U8 = 6,
+  MFX_I8 = 7,
+  MFX_U32 = 8,
+  MFX_F64 = 9,
+};
+
+#define MFX_MAX_RANK 8
+#define MFX_EW_MAX_INPUTS 8
+#define MFX_EW_MAX_REGS 32
+#define MFX_EW_MAX_INSTRS 64
+
+/* Instruction set of a fused elementwise program.  Registers hold fp32;
+ * integer values are exact up to 2^24 (the index arithmetic of masks). */
+enum {
+  MFX_EW_LOAD = 0, /* r[dst] = input[a] at the current output index */
+  MFX_EW_CONST,    /* r[dst] = imm */
+  MFX_EW_IOTA,     /* r[dst] = coordinate of the output index along dim a */
+  /* unary: r[dst] = f(r[a]) */
+  MFX_EW_NEG,
+  MFX_EW_ABS,
+  MFX_EW_EXP,
+  MFX_EW_EXPM1,
+  MFX_EW_LOG,
+  MFX_EW_LOG1P,
+  MFX_EW_SQRT,
+  MFX_EW_RSQRT,
+  MFX_EW_TANH,
+  MFX_EW_LOGISTIC,
+  MFX_EW_ERF,
+  MFX_EW_SIN,
+  MFX_EW_COS,
+  MFX_EW_FLOOR,
+  MFX_EW_CEIL,
+  MFX_EW_ROUND_NE,
+  MFX_EW_SIGN,
+  MFX_EW_NOT,        /* logical not (pred) or bitwise not (int flag) */
+  MFX_EW_ROUND_BF16, /* round to the nearest bf16 value (a convert to bf16) */
+  MFX_EW_ROUND_F16,
+  MFX_EW_TO_INT,     /* truncate toward zero (a convert float -> int) */
+  MFX_EW_IS_FINITE,
+  MFX_EW_COPY,
+  /* binary: r[dst] = f(r[a], r[b]) */
+  MFX_EW_ADD,
+  MFX_EW_SUB,
+  MFX_EW_MUL,
+  MFX_EW_DIV, /* int flag: truncating division */
+  MFX_EW_MAX, /* NaN-propagating, as stablehlo.maximum */
+  MFX_EW_MIN,
+  MFX_EW_POW,
+  MFX_EW_REM,
+  MFX_EW_AND,
+  MFX_EW_OR,
+  MFX_EW_XOR,
+  MFX_EW_EQ,
+  MFX_EW_NE,
+  MFX_EW_LT,
+  MFX_EW_LE,
+  MFX_EW_GT,
+  MFX_EW_GE,
+  MFX_EW_ATAN2,
+  /* ternary */
+  MFX_EW_SELECT, /* r[dst] = r[a] != 0 ? r[b] : r[c] */
+  MFX_EW_CLAMP,  /* r[dst] = min(max(r[b], r[a]), r[c]) */
+  MFX_EW_NUM_OPS
+};
+
+#define MFX_EW_FLAG_INT 1 /* integer semantics for DIV / REM / AND / OR / XOR / NOT */
+
+typedef struct {
+  uint8_t op;
+  uint8_t dst;
+  uint8_t a;
+  uint8_t b;
+  uint8_t c;
+  uint8_t flags;
+  uint8_t pad[2];
+  float imm;
+} mfx_ew_instr;
+
+typedef struct {
+  const void* data;
+  int32_t dtype;
+  int32_t pad;
+  int64_t strides[MFX_MAX_RANK]; /* element strides per output dim; 0 broadcasts */
+} mfx_ew_input;
+
+/* out[idx] = program(inputs at idx) for every index of a [dims] output,
+ * stored as out_dtype at element offset sum(idx[d] * out_strides[d]), or
+ * contiguously (row-major) when every out_strides entry is 0. */
+typedef struct {
+  void* out;
+  int32_t out_dtype;
+  int32_t rank;
+  int64_t dims[MFX_MAX_RANK];
+  int64_t out_strides[MFX_MAX_RANK];
+  int32_t num_inputs;
+  int32_t num_instrs;
+  int32_t result;
+  int32_t pad;
+  mfx_ew_input inputs[MFX_EW_MAX_INPUTS];
+  mfx_ew_instr code[MFX_EW_MAX_INSTRS];
+} mfx_ew_program;
+
+int mfx_elementwise(const mfx_ew_program* prog, void* stream);
+
+enum { MFX_RED_SUM = 0, MFX_RED_MAX = 1, MFX_RED_MIN = 2, MFX_RED_PROD = 3 };
+
+/* out[kept...] = init (op) reduce_{dims d with bit d of reduce_mask}(in),
+ * accumulated in fp32 and stored contiguously over the kept dims in order
+ * (reference reduce handler src/jax_mlx_pjrt.cpp:4896-4999). */
+typedef struct {
+  const void* in;
+  void* out;
+  int32_t in_dtype;
+  int32_t out_dtype;
+  int32_t rank;
+  int32_t op;
+  int64_t dims[MFX_MAX_RANK];
+  int64_t strides[MFX_MAX_RANK];
+  uint32_t reduce_mask;
+  float init;
+} mfx_reduce_args;
+
+int mfx_reduce(const mfx_reduce_args* args, void* stream);
+
+/* Batched GEMM, row-major: for each batch i,
+ *   C_i[m,n] = sum_k op(A_i)[m,k] * op(B_i)[k,n]
+ * with A_i at a + i*stride_a stored [m][k] (lda) or, if trans_a, [k][m];
+ * B_i at b + i*stride_b stored [k][n] (ldb) or, if trans_b, [n][k].
+ * fp32 accumulation; a/b share `dtype`, c has `c_dtype`.
+ * Replaces the dot_general lowering (reference src/jax_mlx_pjrt.cpp:4577-4666). */
+typedef struct {
+  const void* a;
+  const void* b;
+  void* c;
+  int32_t dtype;
+  int32_t c_dtype;
+  int64_t batch, m, n, k;
+  int64_t lda, ldb, ldc;
+  int64_t stride_a, stride_b, stride_c;
+  int32_t trans_a;
+  int32_t trans_b;
+} mfx_gemm_args;
+
+int mfx_gemm(const mfx_gemm_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -626,7 +626,7 @@ typedef struct PJRT_Api {
 #undef PJRT_STUB
 
 /* Number of function slots in the 0.90 table (checked by the plugin). */
-#define PJRT_ABI_NUM_SLOTS 137
+#define PJRT_ABI_NUM_SLOTS 128
 
 #ifdef __cplusplus
 }
