@@ -198,6 +198,57 @@ def bench_config5(torch, native, steps, warmup, rotate=2):
             "kernel": native.sdpa_kernel_name(q, kvs[0][0], kvs[0][1], mask=mask, q_rms_eps=1e-6)}
 
 
+def bench_config4(torch, steps, warmup):
+    """4-layer pre-LN transformer forward (f32, d 512, 8 heads, MLP 2048,
+    x [32,256,512]) compiled from StableHLO text and run through the PJRT C
+    API (Client_Compile, LoadedExecutable_Execute) on device-resident
+    buffers.  Xavier-uniform weights, zero biases, unit LayerNorm scales.
+    Timed with the host clock around `steps` back-to-back Executes (the
+    plugin runs them in order on its own stream) and one final event wait."""
+    import math
+
+    import mlir_modules
+    from jax_mlx_amd import pjrt
+
+    layers, B, T, d, heads, mlp = 4, 32, 256, 512, 8, 2048
+    client = pjrt.Client()
+    t0 = time.perf_counter()
+    exe = client.compile(mlir_modules.transformer_module(layers=layers, B=B, T=T, d=d, heads=heads, mlp=mlp))
+    compile_s = time.perf_counter() - t0
+    gen = torch.Generator(device="cuda").manual_seed(4)
+
+    def xavier(fi, fo):
+        a = math.sqrt(6.0 / (fi + fo))
+        return (torch.rand(fi, fo, device="cuda", generator=gen) * 2 - 1) * a
+
+    tensors = [torch.randn(B, T, d, device="cuda", generator=gen)]
+    for _ in range(layers):
+        tensors += [torch.ones(d, device="cuda"), torch.zeros(d, device="cuda"), xavier(d, 3 * d),
+                    torch.zeros(3 * d, device="cuda"), xavier(d, d), torch.zeros(d, device="cuda"),
+                    torch.ones(d, device="cuda"), torch.zeros(d, device="cuda"), xavier(d, mlp),
+                    torch.zeros(mlp, device="cuda"), xavier(mlp, d), torch.zeros(d, device="cuda")]
+    torch.cuda.synchronize()
+    bufs = [client.buffer_view(t) for t in tensors]
+    for _ in range(warmup):
+        exe.execute(bufs)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        outs = exe.execute(bufs, wait=(i == steps - 1))
+    dt = (time.perf_counter() - t0) / steps
+    y = outs[0].to_torch()
+    finite = bool(torch.isfinite(y).all())
+    flops = mlir_modules.transformer_flops(layers=layers, B=B, T=T, d=d, heads=heads, mlp=mlp)
+    res = {"ms_per_module": dt * 1e3, "module_fwd_per_s": 1.0 / dt, "block_fwd_per_s": layers / dt,
+           "flops_per_module": flops, "TFLOPs": flops / dt / 1e12,
+           "frac_fp32_peak": flops / dt / 1e12 / PEAK_FP32_TFLOPS, "compile_s": round(compile_s, 3),
+           "plan_steps": len(client.api.inspect(mlir_modules.transformer_module())["plan"]["steps"]),
+           "output_finite": finite}
+    del outs, bufs
+    exe.destroy()
+    client.destroy()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -268,6 +319,9 @@ def main() -> int:
         extra["config2_sdpa_f32"] = bench_config2(torch, native, 200, 20)
         log("config 5: GQA decode bf16 + RMSNorm(q)")
         extra["config5_decode"] = bench_config5(torch, native, 50, 5)
+        torch.cuda.empty_cache()
+        log("config 4: 4-layer transformer forward through PJRT")
+        extra["config4_transformer_pjrt"] = bench_config4(torch, 20, 3)
         torch.cuda.empty_cache()
         line["extra"] = extra
 

@@ -169,7 +169,16 @@ struct PJRT_TopologyDescription {
   std::vector<PJRT_DeviceDescription*> descs;
 };
 
+// The client is reference counted: Client_Destroy drops the owner's reference
+// and every buffer and loaded executable holds one, so buffers a caller frees
+// after the client (jaxlib's teardown order is not guaranteed, nor is
+// Python's garbage collection) still return their memory to a live pool.
 struct PJRT_Client {
+  std::atomic<int> refs{1};
+  void ref() { ++refs; }
+  void unref() {
+    if (--refs == 0) delete this;
+  }
   std::vector<std::unique_ptr<PJRT_Device>> devices;
   std::vector<std::unique_ptr<PJRT_Memory>> memories;
   std::vector<PJRT_Device*> device_ptrs;
@@ -216,8 +225,32 @@ struct PJRT_Client {
   }
 };
 
+// One counted reference to a client.
+class ClientRef {
+ public:
+  ClientRef() = default;
+  ClientRef(const ClientRef&) = delete;
+  ClientRef& operator=(const ClientRef&) = delete;
+  ~ClientRef() { reset(); }
+  ClientRef& operator=(PJRT_Client* c) {
+    if (c) c->ref();
+    reset();
+    p_ = c;
+    return *this;
+  }
+  void reset() {
+    if (p_) p_->unref();
+    p_ = nullptr;
+  }
+  PJRT_Client* operator->() const { return p_; }
+  operator PJRT_Client*() const { return p_; }
+
+ private:
+  PJRT_Client* p_ = nullptr;
+};
+
 struct PJRT_Buffer {
-  PJRT_Client* client = nullptr;
+  ClientRef client;
   PJRT_Device* device = nullptr;
   void* ptr = nullptr;
   size_t bytes = 0;
@@ -260,7 +293,7 @@ struct PJRT_Executable {
 
 struct PJRT_LoadedExecutable {
   PJRT_Executable* exe = nullptr;
-  PJRT_Client* client = nullptr;
+  ClientRef client;
   bool deleted = false;
 };
 
@@ -520,7 +553,7 @@ PJRT_Error* Client_Create(PJRT_Client_Create_Args* args) {
 
 PJRT_Error* Client_Destroy(PJRT_Client_Destroy_Args* args) {
   CHECK_ARGS(PJRT_Client_Destroy_Args, client);
-  delete args->client;
+  if (args->client) args->client->unref();
   return nullptr;
 }
 

@@ -195,6 +195,38 @@ class Planner {
     return nvals_ + (int)temp_types_.size() - 1;
   }
 
+  // Plan-time bounds proof: every element a step will touch, given its dims,
+  // strides and offset, lies inside the buffer of the value it names.  A
+  // planning mistake then fails Compile instead of faulting on the device.
+  int64_t numel_of(int v) const {
+    const int64_t eb = dtype_bytes(ty(v).dtype);
+    return eb > 0 ? bytes_of(v) / eb : 0;
+  }
+  void check_access(const char* what, int v, int64_t off, const std::vector<int64_t>& dims,
+                    const std::vector<int64_t>& strides) const {
+    int64_t lo = off, hi = off;
+    for (size_t d = 0; d < dims.size(); ++d) {
+      if (dims[d] <= 0) return;  // nothing is accessed
+      const int64_t span = (dims[d] - 1) * strides[d];
+      if (span < 0) lo += span;
+      else hi += span;
+    }
+    if (lo < 0 || hi >= numel_of(v))
+      throw ParseError(std::string("internal: planned ") + what + " access [" + std::to_string(lo) + ", " +
+                       std::to_string(hi) + "] lies outside a buffer of " + std::to_string(numel_of(v)) +
+                       " elements");
+  }
+  void check_access(const char* what, int v, int64_t off, const int64_t* dims, const int64_t* strides,
+                    int rank) const {
+    check_access(what, v, off, std::vector<int64_t>(dims, dims + rank),
+                 std::vector<int64_t>(strides, strides + rank));
+  }
+  void check_dense(const char* what, int v, int64_t numel) const {
+    if (numel > numel_of(v))
+      throw ParseError(std::string("internal: planned ") + what + " of " + std::to_string(numel) +
+                       " elements exceeds its buffer of " + std::to_string(numel_of(v)));
+  }
+
   static void check_supported(const Node& n) {
     static const std::set<std::string> ok = {
         "stablehlo.dot_general", "stablehlo.dot", "stablehlo.reduce", "mfx.sdpa", "mfx.layer_norm",
@@ -489,7 +521,9 @@ class Planner {
       if (dt < 0) throw ParseError("unsupported element type in elementwise input");
       prog.inputs[i].dtype = dt;
       for (int d = 0; d < pb.rank; ++d) prog.inputs[i].strides[d] = pb.ins[i].strides[d];
+      check_access("elementwise load", pb.ins[i].value, pb.ins[i].off, prog.dims, prog.inputs[i].strides, pb.rank);
     }
+    check_dense("elementwise result", out_value, t.numel());
     auto ins = pb.ins;
     StepIO io;
     for (auto& in : ins) io.reads.push_back(in.value);
@@ -673,6 +707,13 @@ class Planner {
     g.stride_c = M * N;
     g.trans_a = A.trans ? 1 : 0;
     g.trans_b = B.trans ? 1 : 0;
+    // Row-major A(m, k) sits at m*lda + k, or k*lda + m when transposed;
+    // B(k, n) at k*ldb + n, or n*ldb + k when transposed.
+    check_access("gemm A", A.value, A.offset, {batch, M, K},
+                 {g.stride_a, A.trans ? 1 : g.lda, A.trans ? g.lda : 1});
+    check_access("gemm B", B.value, B.offset, {batch, K, N},
+                 {g.stride_b, B.trans ? 1 : g.ldb, B.trans ? g.ldb : 1});
+    check_dense("gemm C", out_v, batch * M * N);
     // Row-major B[k][n] wants n unit stride; `layout` reports trans when k is unit.
     StepIO io;
     io.reads = {A.value, B.value};
@@ -718,6 +759,8 @@ class Planner {
     prog.result = 0;
     prog.out_dtype = mfx_dtype(tt.dtype);
     const int base = sv.base;
+    check_access("canonical copy load", base, sv.offset, prog.dims, prog.inputs[0].strides, prog.rank);
+    check_dense("canonical copy", tmp, tt.numel());
     const int64_t off = sv.offset * dtype_bytes(ty(sv.base).dtype);
     auto loc = loc_;
     Plan* plan = &plan_;
@@ -760,6 +803,8 @@ class Planner {
     a.out_dtype = mfx_dtype(ty(n.out[0]).dtype);
     if (a.in_dtype < 0 || a.out_dtype < 0) throw ParseError("reduce dtype not supported");
     const int base = sv.base, out_v = n.out[0];
+    check_access("reduce input", base, sv.offset, a.dims, a.strides, a.rank);
+    check_dense("reduce result", out_v, ty(out_v).numel());
     const int64_t off = sv.offset * dtype_bytes(ty(base).dtype);
     auto loc = loc_;
     Plan* plan = &plan_;
@@ -793,6 +838,10 @@ class Planner {
     a.dtype = mfx_dtype(t.dtype);
     a.param_dtype = gamma >= 0 ? mfx_dtype(ty(gamma).dtype) : beta >= 0 ? mfx_dtype(ty(beta).dtype) : a.dtype;
     if (gamma >= 0 && beta >= 0 && ty(gamma).dtype != ty(beta).dtype) throw ParseError("gamma/beta dtypes differ");
+    check_dense("norm input", x, a.rows * a.n);
+    check_dense("norm result", out_v, a.rows * a.n);
+    if (gamma >= 0) check_dense("norm gamma", gamma, a.n);
+    if (beta >= 0) check_dense("norm beta", beta, a.n);
     int which = n.op == "mfx.layer_norm" ? 0 : n.op == "mfx.rms_norm" ? 1 : 2;
     auto loc = loc_;
     Plan* plan = &plan_;
@@ -908,6 +957,17 @@ class Planner {
       wt.dims = {(int64_t)ws};
       ws_v = new_temp(wt);
     }
+    if (ty(k).dtype != dt || ty(v).dtype != dt || ty(out_v).dtype != dt)
+      throw ParseError("internal: sdpa operand dtypes differ");
+    check_access("sdpa q", q, offs[0], {a.B, a.Hq, a.Tq, a.D}, std::vector<int64_t>(a.q_strides, a.q_strides + 4));
+    check_access("sdpa k", k, offs[1], {a.B, a.Hkv, a.Tk, a.D}, std::vector<int64_t>(a.k_strides, a.k_strides + 4));
+    check_access("sdpa v", v, offs[2], {a.B, a.Hkv, a.Tk, a.Dv},
+                 std::vector<int64_t>(a.v_strides, a.v_strides + 4));
+    check_access("sdpa out", out_v, 0, {a.B, a.Hq, a.Tq, a.Dv}, std::vector<int64_t>(a.o_strides, a.o_strides + 4));
+    if (mask >= 0)
+      check_access("sdpa mask", mask, moff, {a.B, a.Hq, a.Tq, a.Tk},
+                   std::vector<int64_t>(a.mask_strides, a.mask_strides + 4));
+    if (wq >= 0) check_dense("sdpa q-norm weight", wq, a.D);
     const int eb = dtype_bytes(dt);
     const int64_t qo = offs[0] * eb, ko = offs[1] * eb, vo = offs[2] * eb;
     const int64_t mo = moff * (mask >= 0 ? dtype_bytes(ty(mask).dtype) : 0);
@@ -965,6 +1025,8 @@ class Planner {
       prog.num_instrs = 1;
       prog.result = 0;
       prog.out_dtype = mfx_dtype(ot.dtype);
+      check_dense("concatenate operand", in, it.numel());
+      check_access("concatenate store", out_v, pos * cs[dim], prog.dims, prog.out_strides, prog.rank);
       const int64_t off = pos * cs[dim] * dtype_bytes(ot.dtype);
       pos += it.dims[dim];
       auto loc = loc_;

@@ -598,102 +598,142 @@ View trace_view(Ctx& c, int v, bool allow_broadcast) { return mfxp::trace_view(c
 
 // ---- mask expressions: causal detection by evaluation over (t, s) -----------------
 
-// Evaluates a boolean/float elementwise expression at coordinates `coord` of
-// value v, if it depends only on iotas and constants.  Returns false when a
-// non-constant leaf is reached.
-bool eval_const_expr(Ctx& c, int v, const std::vector<int64_t>& coord, double& out, int depth = 0) {
+// Evaluates one row (fixed t, all s) of an elementwise expression that depends
+// only on iotas and constants.  role[d] says what dim d of value v follows:
+// 0 = the query index t, 1 = the key index s, -1 = a fixed coordinate fixed[d].
+// Sets *other when the value would vary along a fixed dim (an iota over it or
+// a non-splat constant spanning it), so the caller knows the predicate is not
+// the same for every batch/head.  Returns false on a non-constant leaf or an
+// op outside the evaluated set.
+bool eval_row(Ctx& c, int v, const std::vector<int>& role, const std::vector<int64_t>& fixed, int64_t t,
+              int64_t S, std::vector<double>& out, bool* other, int depth = 0) {
   if (depth > 64) return false;
   Node* n = c.def(v);
   if (!n) return false;
   const std::string& op = n->op;
+  out.assign((size_t)S, 0.0);
   if (op == "stablehlo.constant") {
     const Literal& l = *n->literal;
     if (l.splat) {
-      out = l.values[0];
+      std::fill(out.begin(), out.end(), l.values[0]);
       return true;
     }
-    auto st = contiguous(l.type.dims);
-    int64_t off = 0;
-    for (size_t i = 0; i < coord.size(); ++i) off += coord[i] * st[i];
-    out = l.values.at(off);
+    const auto& dims = l.type.dims;
+    auto st = contiguous(dims);
+    int64_t base = 0, s_stride = 0;
+    for (size_t d = 0; d < dims.size(); ++d) {
+      if (role[d] == 0) base += t * st[d];
+      else if (role[d] == 1) s_stride += st[d];
+      else {
+        if (dims[d] > 1) *other = true;
+        base += fixed[d] * st[d];
+      }
+    }
+    for (int64_t s = 0; s < S; ++s) out[s] = l.values.at(base + s * s_stride);
     return true;
   }
   if (op == "stablehlo.iota") {
-    out = (double)coord.at(n->ints["dim"].at(0));
+    const int d = (int)n->ints["dim"].at(0);
+    if (role[d] == 1)
+      for (int64_t s = 0; s < S; ++s) out[s] = (double)s;
+    else {
+      if (role[d] == -1 && c.ty(v).dims[d] > 1) *other = true;
+      std::fill(out.begin(), out.end(), role[d] == 0 ? (double)t : (double)fixed[d]);
+    }
     return true;
   }
-  if (op == "stablehlo.broadcast_in_dim") {
-    const auto& bd = n->ints["dims"];
+  if (op == "stablehlo.broadcast_in_dim" || op == "stablehlo.transpose" || op == "stablehlo.reshape") {
     const Type& it = c.ty(n->in[0]);
-    std::vector<int64_t> ic(bd.size());
-    for (size_t i = 0; i < bd.size(); ++i) ic[i] = it.dims[i] == 1 ? 0 : coord[bd[i]];
-    return eval_const_expr(c, n->in[0], ic, out, depth + 1);
-  }
-  if (op == "stablehlo.reshape") {
-    const Type& ot = c.ty(v);
-    const Type& it = c.ty(n->in[0]);
-    auto os = contiguous(ot.dims);
-    int64_t lin = 0;
-    for (size_t i = 0; i < coord.size(); ++i) lin += coord[i] * os[i];
-    std::vector<int64_t> ic(it.dims.size());
-    for (int i = (int)it.dims.size() - 1; i >= 0; --i) {
-      ic[i] = lin % it.dims[i];
-      lin /= it.dims[i];
+    std::vector<int> ir(it.dims.size(), -1);
+    std::vector<int64_t> ifx(it.dims.size(), 0);
+    if (op == "stablehlo.broadcast_in_dim") {
+      const auto& bd = n->ints["dims"];
+      for (size_t i = 0; i < bd.size(); ++i)
+        if (it.dims[i] != 1) {
+          ir[i] = role[bd[i]];
+          ifx[i] = fixed[bd[i]];
+        }
+    } else if (op == "stablehlo.transpose") {
+      const auto& perm = n->ints["dims"];
+      for (size_t i = 0; i < perm.size(); ++i) {
+        ir[perm[i]] = role[i];
+        ifx[perm[i]] = fixed[i];
+      }
+    } else {
+      // Only reshapes that insert or drop unit dims keep a per-dim mapping.
+      const Type& ot = c.ty(v);
+      size_t j = 0;
+      for (size_t i = 0; i < it.dims.size(); ++i) {
+        if (it.dims[i] == 1) continue;
+        while (j < ot.dims.size() && ot.dims[j] == 1) ++j;
+        if (j == ot.dims.size() || ot.dims[j] != it.dims[i]) return false;
+        ir[i] = role[j];
+        ifx[i] = fixed[j];
+        ++j;
+      }
+      for (; j < ot.dims.size(); ++j)
+        if (ot.dims[j] != 1) return false;
     }
-    return eval_const_expr(c, n->in[0], ic, out, depth + 1);
-  }
-  if (op == "stablehlo.transpose") {
-    const auto& perm = n->ints["dims"];
-    std::vector<int64_t> ic(perm.size());
-    for (size_t i = 0; i < perm.size(); ++i) ic[perm[i]] = coord[i];
-    return eval_const_expr(c, n->in[0], ic, out, depth + 1);
+    return eval_row(c, n->in[0], ir, ifx, t, S, out, other, depth + 1);
   }
   if (op == "stablehlo.convert") {
-    if (!eval_const_expr(c, n->in[0], coord, out, depth + 1)) return false;
-    if (c.ty(v).dtype == DType::kPred) out = out != 0.0;
+    if (!eval_row(c, n->in[0], role, fixed, t, S, out, other, depth + 1)) return false;
+    if (c.ty(v).dtype == DType::kPred)
+      for (auto& x : out) x = x != 0.0;
     return true;
   }
-  std::vector<double> a(n->in.size());
-  for (size_t i = 0; i < n->in.size(); ++i)
-    if (!eval_const_expr(c, n->in[i], coord, a[i], depth + 1)) return false;
+  const size_t na = n->in.size();
+  if (na < 1 || na > 3) return false;
+  std::vector<double> a[3];
+  for (size_t i = 0; i < na; ++i)
+    if (!eval_row(c, n->in[i], role, fixed, t, S, a[i], other, depth + 1)) return false;
+  auto each = [&](auto f) {
+    for (int64_t s = 0; s < S; ++s) out[s] = f(s);
+  };
   if (op == "stablehlo.compare") {
     const std::string& d = n->strs["comparison_direction"];
-    out = d == "EQ" ? a[0] == a[1] : d == "NE" ? a[0] != a[1] : d == "LT" ? a[0] < a[1]
-        : d == "LE" ? a[0] <= a[1] : d == "GT" ? a[0] > a[1] : a[0] >= a[1];
+    const auto& x = a[0];
+    const auto& y = a[1];
+    if (d == "EQ") each([&](int64_t s) { return (double)(x[s] == y[s]); });
+    else if (d == "NE") each([&](int64_t s) { return (double)(x[s] != y[s]); });
+    else if (d == "LT") each([&](int64_t s) { return (double)(x[s] < y[s]); });
+    else if (d == "LE") each([&](int64_t s) { return (double)(x[s] <= y[s]); });
+    else if (d == "GT") each([&](int64_t s) { return (double)(x[s] > y[s]); });
+    else if (d == "GE") each([&](int64_t s) { return (double)(x[s] >= y[s]); });
+    else return false;
     return true;
   }
-  if (op == "stablehlo.and") { out = (a[0] != 0) && (a[1] != 0); return true; }
-  if (op == "stablehlo.or") { out = (a[0] != 0) || (a[1] != 0); return true; }
-  if (op == "stablehlo.not") { out = a[0] == 0; return true; }
-  if (op == "stablehlo.select") { out = a[0] != 0 ? a[1] : a[2]; return true; }
-  if (op == "stablehlo.add") { out = a[0] + a[1]; return true; }
-  if (op == "stablehlo.subtract") { out = a[0] - a[1]; return true; }
-  if (op == "stablehlo.multiply") { out = a[0] * a[1]; return true; }
-  if (op == "stablehlo.negate") { out = -a[0]; return true; }
-  if (op == "stablehlo.maximum") { out = std::max(a[0], a[1]); return true; }
-  if (op == "stablehlo.minimum") { out = std::min(a[0], a[1]); return true; }
-  return false;
+  if (op == "stablehlo.and") each([&](int64_t s) { return (double)(a[0][s] != 0 && a[1][s] != 0); });
+  else if (op == "stablehlo.or") each([&](int64_t s) { return (double)(a[0][s] != 0 || a[1][s] != 0); });
+  else if (op == "stablehlo.not") each([&](int64_t s) { return (double)(a[0][s] == 0); });
+  else if (op == "stablehlo.select") each([&](int64_t s) { return a[0][s] != 0 ? a[1][s] : a[2][s]; });
+  else if (op == "stablehlo.add") each([&](int64_t s) { return a[0][s] + a[1][s]; });
+  else if (op == "stablehlo.subtract") each([&](int64_t s) { return a[0][s] - a[1][s]; });
+  else if (op == "stablehlo.multiply") each([&](int64_t s) { return a[0][s] * a[1][s]; });
+  else if (op == "stablehlo.negate") each([&](int64_t s) { return -a[0][s]; });
+  else if (op == "stablehlo.maximum") each([&](int64_t s) { return std::max(a[0][s], a[1][s]); });
+  else if (op == "stablehlo.minimum") each([&](int64_t s) { return std::min(a[0][s], a[1][s]); });
+  else return false;
+  return true;
 }
 
 // Is predicate p (shape = scores layout) exactly "s <= t" (causal, top-left)
-// over dims (t_dim, s_dim), independent of every other dim?
+// over dims (t_dim, s_dim) and independent of every other dim?  Every (t, s)
+// is evaluated; independence is shown structurally (no iota or non-splat
+// constant spans another dim).
 bool is_causal_pred(Ctx& c, int p, int t_dim, int s_dim) {
   const Type& pt = c.ty(p);
   const int64_t T = pt.dims[t_dim], S = pt.dims[s_dim];
-  std::vector<int64_t> coord(pt.dims.size(), 0);
-  // Cheap probes over the other dims' first/last coordinates, then the full grid.
-  for (int corner = 0; corner < 2; ++corner) {
-    for (size_t d = 0; d < coord.size(); ++d)
-      if ((int)d != t_dim && (int)d != s_dim) coord[d] = corner ? pt.dims[d] - 1 : 0;
-    for (int64_t t = 0; t < T; ++t)
-      for (int64_t s = 0; s < S; ++s) {
-        if (corner && t % 61 != 0 && t != T - 1) continue;
-        coord[t_dim] = t;
-        coord[s_dim] = s;
-        double r;
-        if (!eval_const_expr(c, p, coord, r)) return false;
-        if ((r != 0.0) != (s <= t)) return false;
-      }
+  std::vector<int> role(pt.dims.size(), -1);
+  role[t_dim] = 0;
+  role[s_dim] = 1;
+  const std::vector<int64_t> fixed(pt.dims.size(), 0);
+  std::vector<double> row;
+  bool other = false;
+  for (int64_t t = 0; t < T; ++t) {
+    if (!eval_row(c, p, role, fixed, t, S, row, &other) || other) return false;
+    for (int64_t s = 0; s < S; ++s)
+      if ((row[s] != 0.0) != (s <= t)) return false;
   }
   return true;
 }

@@ -1,0 +1,253 @@
+"""PJRT plugin tests that need no GPU: the C API table, the exported symbols,
+error behaviour without a device, and what Compile's rewriter and planner do
+to each module form (through mfx_pjrt_inspect).
+
+The pattern decisions mirror the reference's RecognizePatterns cases
+(src/jax_mlx_pjrt.cpp:1857-2044 softmax, :2166-2334 RMSNorm, :2336-2487
+LayerNorm, :2490-2757 SDPA, :8108-8236 custom calls) and its tests of those
+fusions (tests/test_fusion_patterns.py, tests/test_sdpa.py)."""
+import math
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import mlir_modules as M
+from jax_mlx_amd import pjrt
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="module")
+def api():
+    return pjrt.Api()
+
+
+def fused(doc):
+    return [n for n in doc["graph"]["nodes"] if n["op"].startswith("mfx.")]
+
+
+def steps(doc):
+    return [s["kind"] for s in doc["plan"]["steps"]]
+
+
+# ------------------------------------------------------------------ C API table
+
+def test_table_order_matches_header(api):
+    text = (REPO / "include" / "pjrt_abi.h").read_text()
+    body = text[text.index("typedef struct PJRT_Api {"):]
+    body = body[:body.index("} PJRT_Api;")]
+    names = re.findall(r"PJRT_(?:FN|STUB)\(PJRT_(\w+)\)|void \(\*PJRT_(\w+)\)", body)
+    names = [a or b for a, b in names]
+    assert names == pjrt.SLOTS
+    assert len(names) == 128
+
+
+def test_table_header(api):
+    assert api.version == (0, 90)
+    assert api.struct_size == 40 + 8 * len(pjrt.SLOTS)
+    assert all(api.slots.values()), [k for k, v in api.slots.items() if not v]
+
+
+def test_exports():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(pjrt.PLUGIN_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    syms = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    header = (REPO / "include" / "pjrt_mi355x.h").read_text()
+    declared = set(re.findall(r"^\S.*?\b(\w+)\(", header, re.M)) - {"defined"}
+    assert declared == {"GetPjrtApi", "mfx_pjrt_inspect", "mfx_pjrt_free"}
+    assert declared <= syms
+    # nothing of the plugin's internals leaks into the dynamic symbol table
+    assert syms == declared, syms - declared
+
+
+def test_client_create_needs_device(api):
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(pjrt.PjrtError) as e:
+        pjrt.Client(api)
+    assert e.value.code_name == "FAILED_PRECONDITION"
+
+
+def test_unimplemented_slot_reports_error(api):
+    # a stub slot returns an UNIMPLEMENTED PJRT_Error naming itself
+    a = pjrt.new(pjrt.BufferArgs)
+    with pytest.raises(pjrt.PjrtError) as e:
+        api.call("Client_DmaMap", a)
+    assert e.value.code_name == "UNIMPLEMENTED" and "DmaMap" in e.value.message
+
+
+def test_struct_size_checked(api):
+    a = pjrt.new(pjrt.ClientCreateArgs)
+    a.struct_size = 8
+    with pytest.raises(pjrt.PjrtError) as e:
+        api.call("Client_Create", a)
+    assert e.value.code_name == "INVALID_ARGUMENT"
+
+
+# ------------------------------------------------------------ rewriter + planner
+
+@pytest.mark.parametrize("form", ["var", "standardize"])
+def test_layer_norm_forms_fuse_with_affine(api, form):
+    d = api.inspect(M.layer_norm_module(form=form))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.layer_norm"
+    assert n["i:has_gamma"] == [1] and n["i:has_beta"] == [1]
+    assert math.isclose(n["f:eps"], 1e-5, rel_tol=1e-6)
+    assert steps(d) == ["layer_norm"] and d["plan"]["arena_bytes"] == 0
+
+
+def test_layer_norm_flax_bf16(api):
+    d = api.inspect(M.layer_norm_module(shape=(4, 64, 256), dt="bf16", form="flax"))
+    assert [n["op"] for n in fused(d)] == ["mfx.layer_norm"]
+    assert steps(d)[-1] == "layer_norm"
+
+
+def test_layer_norm_without_affine(api):
+    d = api.inspect(M.layer_norm_module(affine=False, eps=1e-6))
+    (n,) = fused(d)
+    assert n["i:has_gamma"] == [0] and n["i:has_beta"] == [0]
+    assert math.isclose(n["f:eps"], 1e-6, rel_tol=1e-6)
+
+
+def test_layer_norm_intermediate_escapes_stays_computed(api):
+    """A matched intermediate (the mean) returned by the function: the
+    reference rejects the fusion (hasExternalConsumers,
+    src/jax_mlx_pjrt.cpp:1819-1855); this rewriter fuses the normalisation
+    and keeps the escaping mean's own ops, so both results are produced."""
+    shape = [4, 128]
+    f = M.Fn("main", [(shape, "f32")])
+    x = f.arg(0)
+    mean, ks = M._mean_keepdims(f, x, shape, "f32")
+    cen = f.binary("subtract", x, f.bcast(mean, ks, [0, 1], shape, "f32"), shape, "f32")
+    var, _ = M._mean_keepdims(f, f.binary("multiply", cen, cen, shape, "f32"), shape, "f32")
+    inv = f.unary("rsqrt", f.binary("add", var, f.splat(1e-5, ks, "f32"), ks, "f32"), ks, "f32")
+    y = f.binary("multiply", cen, f.bcast(inv, ks, [0, 1], shape, "f32"), shape, "f32")
+    text = M.module("m", [f.text([y, mean], [M.ty(shape, "f32"), M.ty(ks, "f32")])])
+    d = api.inspect(text)
+    assert [n["op"] for n in fused(d)] == ["mfx.layer_norm"]
+    assert len(d["graph"]["results"]) == 2
+    assert "reduce" in steps(d) and "layer_norm" in steps(d)
+
+
+def test_rms_norm(api):
+    d = api.inspect(M.rms_norm_module())
+    (n,) = fused(d)
+    assert n["op"] == "mfx.rms_norm" and n["i:has_gamma"] == [1]
+    assert math.isclose(n["f:eps"], 1e-6, rel_tol=1e-6)
+    d = api.inspect(M.rms_norm_module(dt="bf16", upcast=True))
+    assert [n["op"] for n in fused(d)] == ["mfx.rms_norm"]
+
+
+def test_softmax_through_func_call(api):
+    d = api.inspect(M.softmax_module())
+    assert [n["op"] for n in fused(d)] == ["mfx.softmax"] and steps(d) == ["softmax"]
+
+
+def test_softmax_on_leading_axis_is_not_fused(api):
+    shape = [64, 6]
+    f = M.Fn("main", [(shape, "f32")])
+    x = f.arg(0)
+    m, ms = f.reduce(x, shape, [0], "maximum", "f32")
+    e = f.unary("exponential", f.binary("subtract", x, f.bcast(m, ms, [1], shape, "f32"), shape, "f32"),
+                shape, "f32")
+    z, zs = f.reduce(e, shape, [0], "add", "f32")
+    y = f.binary("divide", e, f.bcast(z, zs, [1], shape, "f32"), shape, "f32")
+    d = api.inspect(M.module("m", [f.text([y], [M.ty(shape, "f32")])]))
+    assert fused(d) == []
+    assert "reduce" in steps(d)
+
+
+def test_sdpa_config2(api):
+    d = api.inspect(M.sdpa_bhtd_module())
+    (n,) = fused(d)
+    assert n["op"] == "mfx.sdpa"
+    assert n["i:shape"] == [8, 8, 8, 128, 128, 64, 64]  # B Hq Hkv Tq Tk D Dv
+    assert n["i:causal"] == [0] and n["i:mask_kind"] == [0]
+    assert math.isclose(n["f:scale"], 0.125, rel_tol=1e-6)
+    assert steps(d) == ["sdpa"]
+
+
+def test_sdpa_config3_causal_bhtd(api):
+    d = api.inspect(M.sdpa_bhtd_module(B=4, H=32, T=2048, D=128, dt="bf16", causal=True))
+    (n,) = fused(d)
+    assert n["i:causal"] == [1] and n["i:shape"] == [4, 32, 32, 2048, 2048, 128, 128]
+
+
+def test_sdpa_jax_nn_form_causal(api):
+    d = api.inspect(M.dot_product_attention_module())
+    (n,) = fused(d)
+    assert n["i:causal"] == [1]
+    # output written straight into the BTNH result: strides of [B, N, T, H] view
+    assert n["i:o_strides"] == [2048 * 32 * 128, 128, 32 * 128, 1]
+    assert steps(d) == ["sdpa"]
+
+
+def test_sdpa_anti_causal_predicate_becomes_mask(api):
+    """A lower-right/other predicate is not the causal one: it stays a mask."""
+    T = 32
+    text = M.sdpa_bhtd_module(B=1, H=2, T=T, D=64, causal=True)
+    text = text.replace("GE,", "LE,")
+    d = api.inspect(text)
+    sd = [n for n in fused(d) if n["op"] == "mfx.sdpa"]
+    assert sd and sd[0]["i:causal"] == [0] and sd[0]["i:mask_kind"] == [2]
+
+
+def test_sdpa_finite_mask_value_falls_back(api):
+    """select(pred, s, -1e9) is not treated as causal (the fill is finite):
+    the module runs through the generic ops and softmax instead."""
+    d = api.inspect(M.sdpa_bhtd_module(B=1, H=2, T=16, D=64, causal=True, mask_value=-1e9))
+    assert "mfx.sdpa" not in [n["op"] for n in fused(d)]
+    assert steps(d).count("gemm") == 2
+
+
+def test_sdpa_transposed_k(api):
+    d = api.inspect(M.sdpa_bhtd_module(transposed_k=True, inline_softmax=True))
+    assert [n["op"] for n in fused(d)] == ["mfx.sdpa"]
+    assert steps(d) == ["elementwise", "sdpa"]  # k made contiguous first
+
+
+def test_sdpa_gqa_bias(api):
+    d = api.inspect(M.dot_product_attention_module(B=2, T=64, N=8, K=2, H=64, is_causal=False, bias=True))
+    (n,) = fused(d)
+    assert n["i:shape"][:3] == [2, 8, 2]
+    assert n["i:mask_kind"] == [1] and n["i:mask_strides"] == [64, 0, 0, 1]
+
+
+def test_gqa_decode_with_q_rms(api):
+    d = api.inspect(M.gqa_decode_module())
+    (n,) = fused(d)
+    assert n["i:q_rms"] == [1] and n["i:shape"] == [16, 32, 8, 1, 8192, 128, 128]
+    assert n["i:mask_kind"] == [1]
+    assert steps(d) == ["sdpa"] and d["plan"]["arena_bytes"] > 0  # split-KV workspace
+
+
+def test_custom_calls(api):
+    d = api.inspect(M.custom_call_sdpa_module(scale=0.2))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.sdpa" and math.isclose(n["f:scale"], 0.2, rel_tol=1e-6)
+    assert n["i:o_strides"] == [64 * 4 * 64, 64, 4 * 64, 1]
+    d = api.inspect(M.custom_call_layer_norm_module(eps=1e-3))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.layer_norm" and math.isclose(n["f:eps"], 1e-3, rel_tol=1e-6)
+
+
+def test_transformer_plan(api):
+    d = api.inspect(M.transformer_module(layers=2, B=2, T=64, d=128, heads=4, mlp=256))
+    ops = [n["op"] for n in fused(d)]
+    assert ops.count("mfx.layer_norm") == 4 and ops.count("mfx.sdpa") == 2
+    s = steps(d)
+    assert s.count("gemm") == 8 and s.count("sdpa") == 2 and s.count("layer_norm") == 4
+    sd = [n for n in fused(d) if n["op"] == "mfx.sdpa"][0]
+    assert sd["i:offsets"] == [0, 128, 256, 0]  # q, k, v read in place from the QKV projection
+
+
+def test_parse_errors(api):
+    with pytest.raises(pjrt.PjrtError) as e:
+        api.inspect("module { func.func @main() { stablehlo.while } }")
+    assert e.value.code_name == "INVALID_ARGUMENT" and "while" in e.value.message
+    with pytest.raises(pjrt.PjrtError):
+        api.inspect("not mlir at all")

@@ -1,0 +1,320 @@
+"""End-to-end parity through the PJRT C API: Client_Compile of StableHLO text,
+BufferFromHostBuffer / CreateViewOfDeviceBuffer, LoadedExecutable_Execute,
+Buffer_ToHostBuffer -- the path jaxlib drives -- checked against the fp64
+oracle.
+
+Bars as in the kernel tests: f32 max-abs <= 1e-5 (norms) / 1e-4 (SDPA);
+bf16 ||out - ref||_inf / ||ref||_inf <= 2e-2.  Modules that run through the
+generic ops (rocBLAS GEMMs, the elementwise interpreter, reductions) carry the
+f32 tolerance stated at each test."""
+import math
+
+import numpy as np
+import pytest
+
+import mlir_modules as M
+
+pytestmark = pytest.mark.gpu
+
+F32_NORM_TOL = 1e-5
+F32_SDPA_TOL = 1e-4
+BF16_REL_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def client(cuda):
+    from jax_mlx_amd import pjrt
+
+    c = pjrt.Client()
+    yield c
+    c.destroy()
+
+
+def bf16_round(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).bfloat16().float().numpy()
+
+
+def host_arg(a, dt):
+    """Host tensor for BufferFromHostBuffer in the module's dtype."""
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    return t.bfloat16() if dt == "bf16" else t
+
+
+def run(client, text, arrays, dts):
+    exe = client.compile(text)
+    bufs = [client.buffer_from_host(host_arg(a, dt)) for a, dt in zip(arrays, dts)]
+    outs = exe.execute(bufs)
+    res = [o.to_torch().float().numpy().astype(np.float64) for o in outs]
+    for b in bufs + outs:
+        b.destroy()
+    exe.destroy()
+    return res
+
+
+def rel_inf(out, ref):
+    return np.abs(out - ref).max() / np.abs(ref).max()
+
+
+# ---------------------------------------------------------------- norms
+
+@pytest.mark.parametrize("form", ["var", "standardize"])
+def test_layer_norm_config1(client, oracle, form):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((8, 128, 512)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    (y,) = run(client, M.layer_norm_module(form=form), [x, g, b], ["f32"] * 3)
+    assert np.abs(y - oracle.layer_norm(x, g, b, 1e-5)).max() <= F32_NORM_TOL
+
+
+def test_layer_norm_flax_bf16(client, oracle):
+    rng = np.random.default_rng(11)
+    x = bf16_round(rng.standard_normal((4, 64, 256)) * 2 + 0.5)
+    g = bf16_round(1 + 0.1 * rng.standard_normal(256))
+    b = bf16_round(0.1 * rng.standard_normal(256))
+    (y,) = run(client, M.layer_norm_module(shape=(4, 64, 256), dt="bf16", form="flax"), [x, g, b], ["bf16"] * 3)
+    assert rel_inf(y, oracle.layer_norm(x, g, b, 1e-5)) <= BF16_REL_TOL
+
+
+def test_custom_call_layer_norm(client, oracle):
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((4, 512)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    (y,) = run(client, M.custom_call_layer_norm_module(eps=1e-3), [x, g, b], ["f32"] * 3)
+    assert np.abs(y - oracle.layer_norm(x, g, b, 1e-3)).max() <= F32_NORM_TOL
+
+
+@pytest.mark.parametrize("dt,upcast", [("f32", False), ("bf16", True)])
+def test_rms_norm(client, oracle, dt, upcast):
+    rng = np.random.default_rng(13)
+    x = bf16_round(rng.standard_normal((2, 4, 128)))
+    w = bf16_round(1 + 0.1 * rng.standard_normal(128))
+    (y,) = run(client, M.rms_norm_module(dt=dt, upcast=upcast), [x, w], [dt, dt])
+    ref = oracle.rms_norm(x, w, 1e-6)
+    if dt == "f32":
+        assert np.abs(y - ref).max() <= F32_NORM_TOL
+    else:
+        assert rel_inf(y, ref) <= BF16_REL_TOL
+
+
+def test_softmax(client, oracle):
+    rng = np.random.default_rng(14)
+    x = (rng.standard_normal((6, 64)) * 4).astype(np.float32)
+    (y,) = run(client, M.softmax_module(), [x], ["f32"])
+    assert np.abs(y - oracle.softmax(x)).max() <= F32_NORM_TOL
+
+
+# ---------------------------------------------------------------- attention
+
+def test_sdpa_config2(client, oracle):
+    rng = np.random.default_rng(2)
+    q, k, v = (rng.standard_normal((8, 8, 128, 64)).astype(np.float32) for _ in range(3))
+    (o,) = run(client, M.sdpa_bhtd_module(), [q, k, v], ["f32"] * 3)
+    assert np.abs(o - oracle.sdpa(q, k, v, 0.125)).max() <= F32_SDPA_TOL
+
+
+def test_sdpa_causal_bhtd_bf16(client, oracle):
+    rng = np.random.default_rng(3)
+    q, k, v = (bf16_round(rng.standard_normal((1, 4, 256, 128))) for _ in range(3))
+    (o,) = run(client, M.sdpa_bhtd_module(B=1, H=4, T=256, D=128, dt="bf16", causal=True), [q, k, v], ["bf16"] * 3)
+    assert rel_inf(o, oracle.sdpa(q, k, v, 1 / math.sqrt(128), causal=True)) <= BF16_REL_TOL
+
+
+def test_dot_product_attention_btnh_causal(client, oracle):
+    """jax.nn.dot_product_attention(is_causal=True) layout: BTNH in and out."""
+    rng = np.random.default_rng(3)
+    B, T, N, H = 2, 192, 4, 128
+    q, k, v = (bf16_round(rng.standard_normal((B, T, N, H))) for _ in range(3))
+    (o,) = run(client, M.dot_product_attention_module(B=B, T=T, N=N, H=H), [q, k, v], ["bf16"] * 3)
+    t = lambda a: a.transpose(0, 2, 1, 3)
+    ref = t(oracle.sdpa(t(q), t(k), t(v), 1 / math.sqrt(H), causal=True))
+    assert rel_inf(o, ref) <= BF16_REL_TOL
+
+
+def test_dot_product_attention_gqa_bias(client, oracle):
+    rng = np.random.default_rng(4)
+    B, T, N, K, H = 2, 64, 8, 2, 64
+    q = bf16_round(rng.standard_normal((B, T, N, H)))
+    k, v = (bf16_round(rng.standard_normal((B, T, K, H))) for _ in range(2))
+    bias = np.where(rng.random((B, 1, 1, T)) < 0.2, -1e9, 0.0).astype(np.float32)
+    bias[:, ..., 0] = 0.0
+    (o,) = run(client, M.dot_product_attention_module(B=B, T=T, N=N, K=K, H=H, is_causal=False, bias=True),
+               [q, k, v, bias], ["bf16"] * 3 + ["f32"])
+    t = lambda a: a.transpose(0, 2, 1, 3)
+    ref = t(oracle.sdpa(t(q), t(k), t(v), 1 / math.sqrt(H), mask=bias))
+    assert rel_inf(o, ref) <= BF16_REL_TOL
+
+
+def test_sdpa_predicate_mask(client, oracle):
+    """A non-causal predicate (s >= t) runs as a fused boolean mask."""
+    rng = np.random.default_rng(5)
+    T = 32
+    q, k, v = (rng.standard_normal((1, 2, T, 64)).astype(np.float32) for _ in range(3))
+    text = M.sdpa_bhtd_module(B=1, H=2, T=T, D=64, causal=True).replace("GE,", "LE,")
+    (o,) = run(client, text, [q, k, v], ["f32"] * 3)
+    keep = np.triu(np.ones((T, T), bool))
+    ref = oracle.sdpa(q, k, v, 0.125, mask=np.where(keep, 0.0, -np.inf)[None, None])
+    assert np.abs(o - ref).max() <= F32_SDPA_TOL
+
+
+def test_sdpa_finite_mask_through_generic_ops(client, oracle):
+    """select(tril, s, -1e9) is not fused: GEMM + select + softmax + GEMM.
+    Tolerance: the f32 SDPA bar (rocBLAS f32 GEMMs accumulate in f32)."""
+    rng = np.random.default_rng(6)
+    q, k, v = (rng.standard_normal((1, 2, 16, 64)).astype(np.float32) for _ in range(3))
+    (o,) = run(client, M.sdpa_bhtd_module(B=1, H=2, T=16, D=64, causal=True, mask_value=-1e9), [q, k, v],
+               ["f32"] * 3)
+    assert np.abs(o - oracle.sdpa(q, k, v, 0.125, causal=True)).max() <= F32_SDPA_TOL
+
+
+def test_sdpa_transposed_k(client, oracle):
+    rng = np.random.default_rng(7)
+    q, v = (rng.standard_normal((2, 2, 128, 64)).astype(np.float32) for _ in range(2))
+    kt = rng.standard_normal((2, 2, 64, 128)).astype(np.float32)
+    (o,) = run(client, M.sdpa_bhtd_module(B=2, H=2, transposed_k=True, inline_softmax=True), [q, kt, v],
+               ["f32"] * 3)
+    ref = oracle.sdpa(q, np.ascontiguousarray(kt.transpose(0, 1, 3, 2)), v, 0.125)
+    assert np.abs(o - ref).max() <= F32_SDPA_TOL
+
+
+def test_custom_call_sdpa_btnh(client, oracle):
+    rng = np.random.default_rng(8)
+    q, k, v = (rng.standard_normal((2, 64, 4, 64)).astype(np.float32) for _ in range(3))
+    (o,) = run(client, M.custom_call_sdpa_module(scale=0.2), [q, k, v], ["f32"] * 3)
+    t = lambda a: a.transpose(0, 2, 1, 3)
+    assert np.abs(o - t(oracle.sdpa(t(q), t(k), t(v), 0.2))).max() <= F32_SDPA_TOL
+
+
+@pytest.mark.parametrize("S", [1024, 8192])
+def test_gqa_decode_with_q_rms(client, oracle, S):
+    """Config 5's module (RMSNorm(q) + GQA + additive padding mask) at batch 4."""
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, D = 4, 32, 8, 128
+    q = bf16_round(rng.standard_normal((B, Hq, 1, D)))
+    k, v = (bf16_round(rng.standard_normal((B, Hkv, S, D))) for _ in range(2))
+    lens = rng.integers(1, S + 1, size=B)
+    mask = np.where(np.arange(S)[None, :] < lens[:, None], 0.0, -1e9).astype(np.float32).reshape(B, 1, 1, S)
+    (o,) = run(client, M.gqa_decode_module(B=B, S=S), [q, k, v, mask], ["bf16"] * 3 + ["f32"])
+    qn = bf16_round(oracle.rms_norm(q, None, 1e-6))
+    ref = oracle.sdpa(qn, k, v, 1 / math.sqrt(D), mask=mask)
+    assert rel_inf(o, ref) <= BF16_REL_TOL
+
+
+# ---------------------------------------------------------------- transformer
+
+def transformer_ref(oracle, x, params, heads, eps=1e-5):
+    """fp64 forward of mlir_modules.transformer_module's network."""
+    x = x.astype(np.float64)
+    B, T, d = x.shape
+    hd = d // heads
+
+    def gelu(u):
+        return 0.5 * u * (1 + np.tanh(math.sqrt(2 / math.pi) * (u + 0.044715 * u ** 3)))
+
+    for p in params:
+        g1, b1, wqkv, bqkv, wo, bo, g2, b2, w1, bm1, w2, bm2 = (a.astype(np.float64) for a in p)
+        h = oracle.layer_norm(x, g1, b1, eps)
+        qkv = h @ wqkv + bqkv
+        q, k, v = (qkv[..., j * d:(j + 1) * d].reshape(B, T, heads, hd).transpose(0, 2, 1, 3) for j in range(3))
+        o = oracle.sdpa(q, k, v, 1 / math.sqrt(hd)).transpose(0, 2, 1, 3).reshape(B, T, d)
+        x = x + o @ wo + bo
+        h = oracle.layer_norm(x, g2, b2, eps)
+        x = x + gelu(h @ w1 + bm1) @ w2 + bm2
+    return x
+
+
+def transformer_params(rng, layers, d, mlp):
+    out = []
+    for _ in range(layers):
+        p = [1 + 0.1 * rng.standard_normal(d), 0.1 * rng.standard_normal(d),
+             rng.standard_normal((d, 3 * d)) / math.sqrt(d), 0.1 * rng.standard_normal(3 * d),
+             rng.standard_normal((d, d)) / math.sqrt(d), 0.1 * rng.standard_normal(d),
+             1 + 0.1 * rng.standard_normal(d), 0.1 * rng.standard_normal(d),
+             rng.standard_normal((d, mlp)) / math.sqrt(d), 0.1 * rng.standard_normal(mlp),
+             rng.standard_normal((mlp, d)) / math.sqrt(mlp), 0.1 * rng.standard_normal(d)]
+        out.append([a.astype(np.float32) for a in p])
+    return out
+
+
+def test_transformer_block_f32(client, oracle):
+    """Config 4's network at a reduced size (2 layers, B2 T64 d128 h4 mlp256).
+    Tolerance 2e-4 max-abs: O(1) activations through 8 f32 GEMMs, 4 LayerNorms
+    and 2 attentions (each step within its own f32 bar)."""
+    rng = np.random.default_rng(4)
+    layers, B, T, d, heads, mlp = 2, 2, 64, 128, 4, 256
+    x = rng.standard_normal((B, T, d)).astype(np.float32)
+    params = transformer_params(rng, layers, d, mlp)
+    flat = [x] + [a for p in params for a in p]
+    (y,) = run(client, M.transformer_module(layers=layers, B=B, T=T, d=d, heads=heads, mlp=mlp), flat,
+               ["f32"] * len(flat))
+    assert np.abs(y - transformer_ref(oracle, x, params, heads)).max() <= 2e-4
+
+
+# ---------------------------------------------------------------- client API
+
+def test_buffers_views_strides_and_reexecution(client, oracle, cuda):
+    torch = cuda
+    rng = np.random.default_rng(9)
+    exe = client.compile(M.layer_norm_module(shape=(64, 256)))
+    assert exe.num_outputs == 1 and exe.output_dims == [(64, 256)]
+    from jax_mlx_amd import pjrt
+
+    assert exe.output_types == [pjrt.F32]
+    g = (1 + 0.1 * rng.standard_normal(256)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(256)).astype(np.float32)
+    gb, bb = client.buffer_from_host(g), client.buffer_from_host(b)
+    for trial in range(2):
+        x = rng.standard_normal((64, 256)).astype(np.float32)
+        # x from a column-major host array through byte_strides
+        xt = torch.from_numpy(np.asfortranarray(x))  # element strides (1, 64)
+        assert xt.stride() == (1, 64)
+        xb = client.buffer_from_host(xt, byte_strides=[4 * s for s in xt.stride()])
+        assert xb.dims == (64, 256) and xb.type == pjrt.F32
+        (y,) = exe.execute([xb, gb, bb])
+        assert np.abs(y.to_torch().numpy() - oracle.layer_norm(x, g, b, 1e-5)).max() <= F32_NORM_TOL
+        # the same through a zero-copy view of a device tensor
+        xd = torch.from_numpy(x).cuda()
+        (y2,) = exe.execute([client.buffer_view(xd), gb, bb])
+        assert np.array_equal(y2.to_torch().numpy(), y.to_torch().numpy())
+    cost = exe.cost_analysis()
+    assert "flops" in cost
+    exe.destroy()
+
+
+def test_buffers_and_executables_outlive_client(cuda):
+    """Destroying the client before its buffers and executables is legal: the
+    plugin keeps the client alive until the last of them is destroyed."""
+    from jax_mlx_amd import pjrt
+
+    c = pjrt.Client()
+    exe = c.compile(M.softmax_module())
+    x = np.arange(6 * 64, dtype=np.float32).reshape(6, 64) / 100
+    xb = c.buffer_from_host(x)
+    (y,) = exe.execute([xb])
+    c.destroy()
+    out = y.to_torch().numpy()
+    np.testing.assert_allclose(out.sum(axis=-1), 1.0, rtol=1e-5)
+    for b in (xb, y):
+        b.destroy()
+    exe.destroy()
+
+
+def test_wrong_argument_count_and_type(client):
+    import torch
+
+    from jax_mlx_amd import pjrt
+
+    exe = client.compile(M.softmax_module())
+    with pytest.raises(pjrt.PjrtError) as e:
+        exe.execute([])
+    assert e.value.code_name == "INVALID_ARGUMENT"
+    bad = client.buffer_from_host(torch.zeros((6, 64), dtype=torch.int32))
+    with pytest.raises(pjrt.PjrtError) as e:
+        exe.execute([bad])
+    assert e.value.code_name == "INVALID_ARGUMENT"
+    exe.destroy()
