@@ -62,6 +62,62 @@ def test_exports():
     assert syms == declared, syms - declared
 
 
+C_HOST = r"""
+#include <dlfcn.h>
+#include <stdio.h>
+#include "pjrt_mi355x.h"
+int main(int argc, char** argv) {
+  void* h = dlopen(argv[1], RTLD_NOW | RTLD_LOCAL);
+  if (!h) return 2;
+  const PJRT_Api* (*get)(void) = (const PJRT_Api* (*)(void))dlsym(h, "GetPjrtApi");
+  const PJRT_Api* api = get();
+  PJRT_Plugin_Initialize_Args init = {PJRT_ABI_SIZE(PJRT_Plugin_Initialize_Args, extension_start)};
+  if (api->PJRT_Plugin_Initialize(&init)) return 3;
+  PJRT_Client_Create_Args cc = {0};
+  cc.struct_size = sizeof cc;
+  PJRT_Error* err = api->PJRT_Client_Create(&cc);
+  int code = 0;
+  if (err) {
+    PJRT_Error_GetCode_Args g = {sizeof g, NULL, err, 0};
+    api->PJRT_Error_GetCode(&g);
+    code = g.code;
+    PJRT_Error_Destroy_Args d = {sizeof d, NULL, err};
+    api->PJRT_Error_Destroy(&d);
+  } else {
+    PJRT_Client_Destroy_Args d = {sizeof d, NULL, cc.client};
+    api->PJRT_Client_Destroy(&d);
+  }
+  printf("%d.%d %d\n", api->pjrt_api_version.major_version, api->pjrt_api_version.minor_version, code);
+  return 0;
+}
+"""
+
+
+def test_c_host_binding(tmp_path):
+    """The C host stub of the integration notes compiles against include/ and
+    drives the table (Client_Create reports FAILED_PRECONDITION without a GPU)."""
+    src = tmp_path / "host.c"
+    src.write_text(C_HOST)
+    exe = tmp_path / "host"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{REPO / 'include'}", str(src), "-o", str(exe),
+                    "-ldl"], check=True)
+    out = subprocess.run([str(exe), str(pjrt.PLUGIN_LIB)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    version, code = out.stdout.split()
+    assert version == "0.90"
+    import torch
+
+    if not torch.cuda.is_available():
+        assert int(code) == 9  # FAILED_PRECONDITION
+
+
+def test_jax_modules_import_without_jax():
+    from jax_mlx_amd import layer_norm, plugin, sdpa
+
+    assert Path(plugin.library_path()) == pjrt.PLUGIN_LIB
+    assert callable(sdpa.mlx_dot_product_attention) and callable(layer_norm.mlx_layer_norm)
+
+
 def test_client_create_needs_device(api):
     import torch
 
