@@ -249,6 +249,30 @@ def bench_config4(torch, steps, warmup):
     return res
 
 
+def bench_copy(torch, steps, warmup, nbytes=1 << 30):
+    """Plain device-to-device copy of `nbytes`: reads and writes exactly
+    nbytes each, the reference point for the FETCH_SIZE / WRITE_SIZE
+    counters of the other kernels."""
+    src = torch.empty(nbytes // 4, device="cuda", dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    avg_ms, med_ms, _ = time_launches(torch, lambda: dst.copy_(src), steps, warmup)
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": avg_ms * 1e3,
+            "GBps": 2 * nbytes / (avg_ms * 1e-3) / 1e9}
+
+
+ONLY = {
+    "config1": lambda torch, native, k, w: bench_config1(torch, native, k, w),
+    "config2": lambda torch, native, k, w: bench_config2(torch, native, k, w),
+    "config3": lambda torch, native, k, w: bench_config3(torch, native, k, w),
+    "config4": lambda torch, native, k, w: bench_config4(torch, k, w),
+    "config5": lambda torch, native, k, w: bench_config5(torch, native, k, w),
+    "ln_sweep": lambda torch, native, k, w: {
+        "sweep": [bench_layer_norm(torch, native, 1 << 20, 512, k, w),
+                  bench_layer_norm(torch, native, 65536, 4096, k, w)]},
+    "copy": lambda torch, native, k, w: bench_copy(torch, k, w),
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,6 +280,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
+    ap.add_argument("--only", choices=sorted(ONLY),
+                    help="run one workload alone and print its figures (for profiler runs); "
+                         "'copy' is a plain 1 GiB device copy used to calibrate HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -271,6 +298,12 @@ def main() -> int:
         return 1
     native.load()
     torch.cuda.synchronize()
+
+    if args.only:
+        res = ONLY[args.only](torch, native, args.steps, args.warmup)
+        res.pop("inputs", None)
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        return 0
 
     log("config 3: causal bf16 flash SDPA [4,32,2048,128]")
     c3 = bench_config3(torch, native, args.steps, args.warmup)

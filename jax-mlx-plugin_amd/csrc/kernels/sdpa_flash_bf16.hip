@@ -1,9 +1,10 @@
 // Flash attention forward, bf16 inputs, fp32 accumulation, gfx950 MFMA.
 //
 // Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each
-// wavefront owns 32 query rows.  K/V stream through LDS in 64-key tiles,
-// double-buffered, with the global loads of tile t+1 in flight while tile t
-// is computed.
+// wavefront owns 32 query rows.  K/V stream through LDS in 64-key tiles, two
+// stages: while tile t is computed, tile t+1 is copied global -> LDS by the
+// asynchronous LDS-DMA loads (global_load_lds_dwordx4: no registers, no
+// VALU), and one vmcnt wait + barrier per tile publishes it.
 //
 // Both products use v_mfma_f32_32x32x16_bf16 and are arranged so that the
 // online softmax needs almost no cross-lane traffic:
@@ -11,17 +12,25 @@
 //                 32x32 accumulator gives lane l query (l % 32) and 16 keys,
 //                 so a query's row max / sum is 16 in-lane values plus one
 //                 exchange with lane l ^ 32.
-//   O^T = V^T P^T A = V^T (LDS holds the V tile transposed), B = P taken
-//                 straight from the S^T accumulator: the contraction index
-//                 (key) is permuted identically in A and B, so the
-//                 accumulator registers are already the B operand.
+//   O^T = V^T P^T A = V^T fragments read from the row-major V tile with the
+//                 transposing LDS read (ds_read_b64_tr_b16: 16 lanes x 4
+//                 keys per read), B = P taken straight from the S^T
+//                 accumulator: the contraction index (key) is permuted
+//                 identically in A and B, so the accumulator registers are
+//                 already the B operand.
 // Each lane also owns one query of O^T, so the online-softmax rescale is a
-// per-lane scalar multiply.
+// per-lane scalar multiply, and it is lazy (see kSlack).
+//
+// Tiles are row-major with 16-byte chunks XOR-swizzled per row, so the K
+// operand reads (8 lanes on 8 rows) and the transposing V reads (4 rows x 32
+// bytes per 16 lanes) are bank-conflict free; the DMA writes 1 KiB runs.
 //
 // Causal tiles past a wavefront's last query are skipped; the blockIdx ->
 // (head, q-block) map runs the longest causal blocks first and keeps the
 // q-blocks of one head on one XCD (blocks are dealt to the 8 XCDs
 // round-robin), so its K/V stay in that XCD's L2.
+#include <type_traits>
+
 #include "sdpa_common.h"
 
 namespace mfx {
@@ -31,26 +40,53 @@ constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kNT = 256;  // threads per workgroup
 
-template <int D>
-struct Cfg {
-  static constexpr int KROW = D + 8;                  // bf16 per K row in LDS (16 B pad)
-  static constexpr int VROW = kBN + 4;                // bf16 per V^T row in LDS (8 B pad)
-  static constexpr int CH = kBN * D / 8 / kNT;        // 16-byte chunks per thread per tile
-  static constexpr int DCH = D / 8;                   // 16-byte chunks per row
-};
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
-  return (a & 0xffffu) | (b << 16);
-}
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
-  return (a >> 16) | (b & 0xffff0000u);
+// Exponent slack of the lazy rescale: the running base of a row's exp2 is
+// only raised when a new score exceeds it by more than this (log2 units), so
+// un-normalised probabilities stay below 2^8 and the O / l rescale runs a
+// handful of times per row instead of once per tile.  The result is exact:
+// O and l always share the same base.
+constexpr float kSlack = 8.0f;
+
+// 16-byte chunk c of tile row r is stored at chunk slot c ^ swz(r).  Rows
+// 8 apart repeat; any 8 consecutive rows use 8 different slots (K reads) and
+// any 4-aligned group of 4 rows uses 4 different slot pairs (V reads).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// s_waitcnt vmcnt(0), other counters left alone: this wave's LDS-DMA
+// loads have landed.
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Copies keys [kb, kb + kBN) x D of one (batch, head) into a swizzled LDS
+// tile.  Instruction i of wave w fills tile chunks (4i + w)*64 .. +63, one
+// 16-byte chunk per lane.  Rows past Tk repeat row Tk - 1 (in bounds; their
+// scores are masked to -inf, so they contribute exactly 0).
+template <int D>
+__device__ __forceinline__ void load_tile(const bf16* base, int64_t row_stride, int kb, int Tk, bf16* lds,
+                                          int wave, int lane) {
+  constexpr int DCH = D / 8;
+  constexpr int LOADS = kBN * DCH / kNT;
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int run = i * 4 + wave;
+    const int lin = run * 64 + lane;
+    const int row = lin / DCH, slot = lin % DCH;
+    const int key = min(kb + row, Tk - 1);
+    __builtin_amdgcn_global_load_lds(base + (int64_t)key * row_stride + (slot ^ swz(row)) * 8,
+                                     (lds_void_t*)(lds + run * 64 * 8), 16, 0, 0);
+  }
 }
 
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
-  using C = Cfg<D>;
-  __shared__ __attribute__((aligned(16))) bf16 k_lds[2][kBN * C::KROW];
-  __shared__ __attribute__((aligned(16))) bf16 vt_lds[2][D * C::VROW];
+  __shared__ __attribute__((aligned(16))) bf16 k0[kBN * D];
+  __shared__ __attribute__((aligned(16))) bf16 v0[kBN * D];
+  __shared__ __attribute__((aligned(16))) bf16 k1[kBN * D];
+  __shared__ __attribute__((aligned(16))) bf16 v1[kBN * D];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -81,6 +117,15 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   const int q0 = mblk * kBM + wave * 32;
   const int qi = q0 + l32;
 
+  int kv_end = Tk;
+  if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kBM));
+  const int ntiles = (kv_end + kBN - 1) / kBN;
+  auto issue = [&](int t, bf16* kl, bf16* vl) {
+    load_tile<D>(kp, ks2, t * kBN, Tk, kl, wave, lane);
+    load_tile<D>(vp, vs2, t * kBN, Tk, vl, wave, lane);
+  };
+  if (ntiles > 0) issue(0, k0, v0);
+
   // Rows past Tq load a valid row and are zeroed, so no load is predicated.
   bf16x8 qf[D / 16];
   {
@@ -93,141 +138,121 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
     }
   }
 
-  int kv_end = Tk;
-  if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kBM));
-  const int ntiles = (kv_end + kBN - 1) / kBN;
-
-  u32x4 kreg[C::CH];
-  u32x4 vreg[C::CH];
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  const int vdc = tid % C::DCH;  // V chunk column (d / 8)
-  const int vkg = tid / C::DCH;  // V key group (C::CH keys)
-
-  auto gload = [&](int t) {
-    const int kb = t * kBN;
-#pragma unroll
-    for (int i = 0; i < C::CH; ++i) {
-      const int c = tid + i * kNT;
-      const int row = c / C::DCH, col = c % C::DCH;
-      const int key = kb + row;
-      u32x4 raw = *reinterpret_cast<const u32x4*>(kp + (int64_t)min(key, Tk - 1) * ks2 + col * 8);
-      kreg[i] = key < Tk ? raw : zero4;
-    }
-#pragma unroll
-    for (int r = 0; r < C::CH; ++r) {
-      const int key = kb + vkg * C::CH + r;
-      u32x4 raw = *reinterpret_cast<const u32x4*>(vp + (int64_t)min(key, Tk - 1) * vs2 + vdc * 8);
-      vreg[r] = key < Tk ? raw : zero4;
-    }
-  };
-
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < C::CH; ++i) {
-      const int c = tid + i * kNT;
-      const int row = c / C::DCH, col = c % C::DCH;
-      *reinterpret_cast<u32x4*>(&k_lds[buf][row * C::KROW + col * 8]) = kreg[i];
-    }
-    // Transpose: vreg[r] holds d = vdc*8 .. +7 of key vkg*CH + r.
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      bf16* dst = &vt_lds[buf][(vdc * 8 + j) * C::VROW + vkg * C::CH];
-      uint32_t w[C::CH];
-#pragma unroll
-      for (int r = 0; r < C::CH; ++r) {
-        w[r] = vreg[r][j >> 1];
-      }
-      if constexpr (C::CH == 4) {
-        u32x2 pk;
-        pk[0] = (j & 1) ? pack_hi(w[0], w[1]) : pack_lo(w[0], w[1]);
-        pk[1] = (j & 1) ? pack_hi(w[2], w[3]) : pack_lo(w[2], w[3]);
-        *reinterpret_cast<u32x2*>(dst) = pk;
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = (j & 1) ? pack_hi(w[0], w[1]) : pack_lo(w[0], w[1]);
-      }
-    }
-  };
-
   f32x16 o[D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-  const float sl2 = p.scale_log2;
+  // Running exp2 base (log2 units, shared by lanes l and l^32) and the
+  // lane's partial row sum.
+  float b_run = -INFINITY, l_run = 0.f;
+  const float sl2 = p.scale_log2;  // > 0 (checked on the host)
 
-  if (ntiles > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
+  // Per-lane LDS offsets (bf16 elements) of the operand reads.
+  const int k_off = l32 * D;            // + mt*32*D, chunk (kk*2 + half) ^ k_sw
+  const int k_sw = swz(l32);
+  const int tj = lane & 15, tg = (lane >> 4) & 1;
+  const int v_row = 4 * half + (tj >> 2);  // + ks*16 + 8*r
+  const int v_sw = swz(v_row);
+  const int v_chunk = tg * 2 + ((tj & 3) >> 1);  // + dt*4
+  const int v_sub = (tj & 1) * 4;
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-    const int kb = t * kBN;
-    const bool active = (q0 < Tq) && (!CAUSAL || kb <= q0 + 31);
-    if (active) {
-      f32x16 s[2];
+  // One 64-key tile for this wave's 32 queries.  EDGE tiles (ragged end,
+  // causal diagonal) mask per element; interior tiles do no mask work.
+  auto compute = [&](const bf16* kl, const bf16* vl, int kb, auto edge_tag) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    f32x16 s[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
+      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(
-              &k_lds[buf][(mt * 32 + l32) * C::KROW + kk * 16 + half * 8]);
-          s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[mt], 0, 0, 0);
-        }
+      for (int kk = 0; kk < D / 16; ++kk) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kl[mt * 32 * D + k_off + ((kk * 2 + half) ^ k_sw) * 8]);
+        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[mt], 0, 0, 0);
       }
-      const bool edge = (kb + kBN > Tk) || (CAUSAL && kb + kBN - 1 > q0);
-      float mx = -INFINITY;
+    }
+    // MASK: scores move to the log2 domain here (scale and mask folded);
+    // otherwise they stay raw and the scale is folded into the exp2 FMA.
+    float mx = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float x = s[mt][i] * sl2;
-          const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-          if constexpr (MASK) {
-            if (qi < Tq && key < Tk)
-              x += kLog2e * load_mask(p.mask, p.mask_dtype,
-                                      b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]);
-          }
-          if (edge && (key >= Tk || (CAUSAL && key > qi))) x = -INFINITY;
-          s[mt][i] = x;
-          mx = fmaxf(mx, x);
+      for (int i = 0; i < 16; ++i) {
+        float x = s[mt][i];
+        const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+        if constexpr (MASK) {
+          x *= sl2;
+          if (qi < Tq && key < Tk)
+            x += kLog2e * load_mask(p.mask, p.mask_dtype,
+                                    b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float base = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - base);
-      m_run = m_new;
+        if constexpr (EDGE) {
+          if (key >= Tk || (CAUSAL && key > qi)) x = -INFINITY;
+        }
+        s[mt][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_l2 = MASK ? mx : mx * sl2;
+    const bool need = m_l2 > b_run + kSlack;
+    if (__ballot(need)) {
+      const float nb = need ? m_l2 : b_run;
+      const float alpha = need ? __builtin_amdgcn_exp2f(b_run - nb) : 1.f;
+      b_run = nb;
       l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-      bf16x8 pb[4];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(s[mt][i] - base);
-          l_run += pv;
-          pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(pv);
-        }
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16* vr = &vt_lds[buf][(dt * 32 + l32) * C::VROW + ks * 16 + half * 4];
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
-          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
-          const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
-        }
     }
-    if (t + 1 < ntiles) lstore(buf ^ 1);
+    const float nbase = b_run == -INFINITY ? 0.f : -b_run;
+    bf16x8 pb[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = MASK ? __builtin_amdgcn_exp2f(s[mt][i] + nbase)
+                              : __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
+        l_run += pv;
+        pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(pv);
+      }
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        // k-slots 0-3: keys ks*16 + 4*half + e; slots 4-7: the same + 8.
+        const bf16* v_lo = vl + (ks * 16 + v_row) * D + ((dt * 4 + v_chunk) ^ v_sw) * 8 + v_sub;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_lo));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_lo + 8 * D));
+        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
+      }
+  };
+
+  auto step = [&](int t, const bf16* kl, const bf16* vl) {
+    const int kb = t * kBN;
+    if (q0 >= Tq || (CAUSAL && kb > q0 + 31)) return;  // nothing of this tile is visible
+    const bool edge = (kb + kBN > Tk) || (CAUSAL && kb + kBN - 1 > q0);
+    if (edge)
+      compute(kl, vl, kb, std::true_type{});
+    else
+      compute(kl, vl, kb, std::false_type{});
+  };
+
+  wait_dma();
+  __syncthreads();
+  // Two stages with distinct LDS arrays (so the compiler's LDS-DMA tracking
+  // sees that the loads in flight never alias the tile being read).
+  for (int t = 0; t < ntiles; t += 2) {
+    if (t + 1 < ntiles) issue(t + 1, k1, v1);
+    step(t, k0, v0);
+    wait_dma();
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    if (t + 2 < ntiles) issue(t + 2, k0, v0);
+    step(t + 1, k1, v1);
+    wait_dma();
     __syncthreads();
   }
 
@@ -251,8 +276,7 @@ template <int D, bool CAUSAL, bool MASK>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   const int nmb = (p.Tq + kBM - 1) / kBM;
   const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
-  hipLaunchKernelGGL((flash_bf16_kernel<D, CAUSAL, MASK>), dim3((unsigned)blocks), dim3(kNT), 0,
-                     s, p);
+  hipLaunchKernelGGL((flash_bf16_kernel<D, CAUSAL, MASK>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
   return launch_status("flash_bf16_kernel");
 }
 
@@ -269,6 +293,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 bool flash_bf16_supports(const SdpaParams& p) {
   if (p.dtype != MFX_BF16) return false;
+  if (!(p.scale_log2 > 0.f)) return false;  // the exp2 FMA folds a positive scale
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
