@@ -52,10 +52,18 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 // O and l always share the same base.
 constexpr float kSlack = 8.0f;
 
-// 16-byte chunk c of tile row r is stored at chunk slot c ^ swz(r).  Rows
-// 8 apart repeat; any 8 consecutive rows use 8 different slots (K reads) and
-// any 4-aligned group of 4 rows uses 4 different slot pairs (V reads).
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// 16-byte chunk c of tile row r is stored at chunk slot c ^ tile_swz<D>(r).  The
+// K operand reads (lanes on consecutive rows, one chunk each) and the
+// transposing V reads (4 rows x 2 chunks per 16 lanes) must spread over all
+// banks whether the LDS serves 128 or 256 bytes per clock: for d = 128 the
+// map is a bijection on each aligned run of 16 rows that is also one-to-one
+// on bits 0-2 for 8 rows and on bits 1-2 and 2-3 for 4 rows; d = 64 rows
+// have only 8 chunks and use a period-8 map.
+template <int D>
+__device__ __forceinline__ int tile_swz(int r) {
+  if constexpr (D == 128) return (r & 3) | (((r ^ (r >> 2)) & 3) << 2);
+  return ((r & 3) << 1) | ((r >> 2) & 1);
+}
 
 // s_waitcnt vmcnt(0), other counters left alone: this wave's LDS-DMA
 // loads have landed.
@@ -76,7 +84,8 @@ __device__ __forceinline__ void load_tile(const bf16* base, int64_t row_stride, 
     const int lin = run * 64 + lane;
     const int row = lin / DCH, slot = lin % DCH;
     const int key = min(kb + row, Tk - 1);
-    __builtin_amdgcn_global_load_lds(base + (int64_t)key * row_stride + (slot ^ swz(row)) * 8,
+    const int sw = tile_swz<D>(row);
+    __builtin_amdgcn_global_load_lds(base + (int64_t)key * row_stride + (slot ^ sw) * 8,
                                      (lds_void_t*)(lds + run * 64 * 8), 16, 0, 0);
   }
 }
@@ -150,10 +159,10 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
 
   // Per-lane LDS offsets (bf16 elements) of the operand reads.
   const int k_off = l32 * D;            // + mt*32*D, chunk (kk*2 + half) ^ k_sw
-  const int k_sw = swz(l32);
+  const int k_sw = tile_swz<D>(l32);
   const int tj = lane & 15, tg = (lane >> 4) & 1;
   const int v_row = 4 * half + (tj >> 2);  // + ks*16 + 8*r
-  const int v_sw = swz(v_row);
+  const int v_sw = tile_swz<D>(v_row), v_sw8 = tile_swz<D>(v_row + 8);
   const int v_chunk = tg * 2 + ((tj & 3) >> 1);  // + dt*4
   const int v_sub = (tj & 1) * 4;
 
@@ -222,9 +231,11 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         // k-slots 0-3: keys ks*16 + 4*half + e; slots 4-7: the same + 8.
-        const bf16* v_lo = vl + (ks * 16 + v_row) * D + ((dt * 4 + v_chunk) ^ v_sw) * 8 + v_sub;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_lo));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_lo + 8 * D));
+        const bf16* v_rows = vl + (ks * 16 + v_row) * D + v_sub;
+        const s16x4 lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_rows + ((dt * 4 + v_chunk) ^ v_sw) * 8));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4_t*)(v_rows + 8 * D + ((dt * 4 + v_chunk) ^ v_sw8) * 8));
         const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
       }
@@ -244,14 +255,20 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   __syncthreads();
   // Two stages with distinct LDS arrays (so the compiler's LDS-DMA tracking
   // sees that the loads in flight never alias the tile being read).
+  // The restrict-qualified parameters give every access of one iteration
+  // scoped no-alias metadata, so the waitcnt pass does not make the tile's
+  // reads wait for the next tile's LDS-DMA writes.
+  auto iter = [&](int t, const bf16* __restrict__ kc, const bf16* __restrict__ vc, bf16* __restrict__ kn,
+                  bf16* __restrict__ vn) {
+    if (t + 1 < ntiles) issue(t + 1, kn, vn);
+    step(t, kc, vc);
+  };
   for (int t = 0; t < ntiles; t += 2) {
-    if (t + 1 < ntiles) issue(t + 1, k1, v1);
-    step(t, k0, v0);
+    iter(t, k0, v0, k1, v1);
     wait_dma();
     __syncthreads();
     if (t + 1 >= ntiles) break;
-    if (t + 2 < ntiles) issue(t + 2, k0, v0);
-    step(t + 1, k1, v1);
+    iter(t + 1, k1, v1, k0, v0);
     wait_dma();
     __syncthreads();
   }
