@@ -3,7 +3,7 @@
 // Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each
 // wavefront owns 32 query rows.  K/V stream through LDS in 64-key tiles, two
 // stages: while tile t is computed, tile t+1 is copied global -> LDS by the
-// asynchronous LDS-DMA loads (global_load_lds_dwordx4: no registers, no
+// asynchronous LDS-DMA loads (buffer_load_dwordx4 ... lds: no registers, no
 // VALU), and one vmcnt wait + barrier per tile publishes it.
 //
 // Both products use v_mfma_f32_32x32x16_bf16 and are arranged so that the
@@ -70,25 +70,45 @@ __device__ __forceinline__ int tile_swz(int r) {
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Copies keys [kb, kb + kBN) x D of one (batch, head) into a swizzled LDS
-// tile.  Instruction i of wave w fills tile chunks (4i + w)*64 .. +63, one
-// 16-byte chunk per lane.  Rows past Tk repeat row Tk - 1 (in bounds; their
-// scores are masked to -inf, so they contribute exactly 0).
+// tile with buffer loads to LDS: the per-lane offsets are loop invariant and
+// the tile start is the scalar offset, so a tile costs LOADS instructions and
+// no address arithmetic.  Instruction i of wave w fills tile chunks
+// (4i + w)*64 .. +63, one 16-byte chunk per lane.  The resource spans the
+// Tk keys of this (batch, head): rows past Tk are out of range and read as
+// zeros (their scores are masked to -inf, so they contribute exactly 0).
 template <int D>
-__device__ __forceinline__ void load_tile(const bf16* base, int64_t row_stride, int kb, int Tk, bf16* lds,
-                                          int wave, int lane) {
-  constexpr int DCH = D / 8;
-  constexpr int LOADS = kBN * DCH / kNT;
+struct TileLoader {
+  static constexpr int DCH = D / 8;
+  static constexpr int LOADS = kBN * DCH / kNT;
+  bf16* base;
+  int nbytes;           // extent of the resource: Tk rows
+  uint32_t voff[LOADS];
+  uint32_t tile_bytes;  // scalar offset step per tile
+
+  __device__ __forceinline__ TileLoader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
+    base = const_cast<bf16*>(b);
+    nbytes = (int)((int64_t)Tk * row_stride * 2);
+    tile_bytes = (uint32_t)(kBN * row_stride * 2);
 #pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int run = i * 4 + wave;
-    const int lin = run * 64 + lane;
-    const int row = lin / DCH, slot = lin % DCH;
-    const int key = min(kb + row, Tk - 1);
-    const int sw = tile_swz<D>(row);
-    __builtin_amdgcn_global_load_lds(base + (int64_t)key * row_stride + (slot ^ sw) * 8,
-                                     (lds_void_t*)(lds + run * 64 * 8), 16, 0, 0);
+    for (int i = 0; i < LOADS; ++i) {
+      const int lin = (i * 4 + wave) * 64 + lane;
+      const int row = lin / DCH, slot = lin % DCH;
+      const int sw = tile_swz<D>(row);
+      voff[i] = (uint32_t)(((int64_t)row * row_stride + (slot ^ sw) * 8) * 2);
+    }
   }
-}
+  // The buffer-resource type exists only for the device target; the host
+  // pass of this translation unit sees an empty body.
+  __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, nbytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + (i * 4 + wave) * 64 * 8), 16, voff[i],
+                                               (uint32_t)t * tile_bytes, 0, 0);
+#endif
+  }
+};
 
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
@@ -129,9 +149,10 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   int kv_end = Tk;
   if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kBM));
   const int ntiles = (kv_end + kBN - 1) / kBN;
+  const TileLoader<D> kload(kp, ks2, Tk, wave, lane), vload(vp, vs2, Tk, wave, lane);
   auto issue = [&](int t, bf16* kl, bf16* vl) {
-    load_tile<D>(kp, ks2, t * kBN, Tk, kl, wave, lane);
-    load_tile<D>(vp, vs2, t * kBN, Tk, vl, wave, lane);
+    kload.load(t, kl, wave);
+    vload.load(t, vl, wave);
   };
   if (ntiles > 0) issue(0, k0, v0);
 
@@ -311,6 +332,8 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 bool flash_bf16_supports(const SdpaParams& p) {
   if (p.dtype != MFX_BF16) return false;
   if (!(p.scale_log2 > 0.f)) return false;  // the exp2 FMA folds a positive scale
+  // Buffer-resource offsets of one head's K/V rows are 31-bit.
+  if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
