@@ -26,9 +26,9 @@
 // bytes per 16 lanes) are bank-conflict free; the DMA writes 1 KiB runs.
 //
 // Causal tiles past a wavefront's last query are skipped; the blockIdx ->
-// (head, q-block) map runs the longest causal blocks first and keeps the
-// q-blocks of one head on one XCD (blocks are dealt to the 8 XCDs
-// round-robin), so its K/V stay in that XCD's L2.
+// (head, q-block) map keeps the q-blocks of one head on one XCD (blocks are
+// dealt to the 8 XCDs round-robin) and issues each XCD's blocks longest
+// first, which balances the causal triangle across the CUs.
 #include <type_traits>
 
 #include "sdpa_common.h"
@@ -37,7 +37,9 @@ namespace mfx {
 namespace {
 
 constexpr int kBM = 128;  // query rows per workgroup
-constexpr int kBN = 64;   // keys per tile
+constexpr int kBN = 64;        // keys per tile
+constexpr int kMT = kBN / 32;  // 32-key score blocks per tile
+constexpr int kKS = kBN / 16;  // 16-key PV steps per tile
 constexpr int kNT = 256;  // threads per workgroup
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -60,7 +62,7 @@ constexpr float kSlack = 8.0f;
 // on bits 0-2 for 8 rows and on bits 1-2 and 2-3 for 4 rows; d = 64 rows
 // have only 8 chunks and use a period-8 map.
 template <int D>
-__device__ __forceinline__ int tile_swz(int r) {
+__host__ __device__ constexpr int tile_swz(int r) {
   if constexpr (D == 128) return (r & 3) | (((r ^ (r >> 2)) & 3) << 2);
   return ((r & 3) << 1) | ((r >> 2) & 1);
 }
@@ -70,32 +72,39 @@ __device__ __forceinline__ int tile_swz(int r) {
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Copies keys [kb, kb + kBN) x D of one (batch, head) into a swizzled LDS
-// tile with buffer loads to LDS: the per-lane offsets are loop invariant and
-// the tile start is the scalar offset, so a tile costs LOADS instructions and
-// no address arithmetic.  Instruction i of wave w fills tile chunks
-// (4i + w)*64 .. +63, one 16-byte chunk per lane.  The resource spans the
-// Tk keys of this (batch, head): rows past Tk are out of range and read as
-// zeros (their scores are masked to -inf, so they contribute exactly 0).
+// tile with buffer loads to LDS.  Instruction i of wave w fills tile chunks
+// (4i + w)*64 .. +63, one 16-byte chunk per lane, i.e. rows
+// (4i + w)*RPI .. +RPI-1 with RPI = 64 / (D/8).  The swizzle repeats every
+// 4*RPI rows (16 for d = 128, 32 for d = 64; its period divides both), so
+// instruction i reads the same per-lane source offset as instruction 0 plus
+// i*4*RPI rows: one VGPR per operand, and the tile start and the step are
+// scalar offsets.  The resource spans the Tk keys of this (batch, head):
+// rows past Tk are out of range and read as zeros (their scores are masked
+// to -inf, so they contribute exactly 0).
 template <int D>
 struct TileLoader {
   static constexpr int DCH = D / 8;
+  static constexpr int RPI = 64 / DCH;  // rows per load instruction
   static constexpr int LOADS = kBN * DCH / kNT;
+  static constexpr bool swz_period_divides(int step) {
+    for (int r = 0; r < kBN; ++r)
+      if (tile_swz<D>(r) != tile_swz<D>(r + step)) return false;
+    return true;
+  }
   bf16* base;
   int nbytes;           // extent of the resource: Tk rows
-  uint32_t voff[LOADS];
+  uint32_t voff;        // per-lane source offset of instruction 0
+  uint32_t step_bytes;  // scalar offset step per instruction
   uint32_t tile_bytes;  // scalar offset step per tile
 
   __device__ __forceinline__ TileLoader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
+    static_assert(swz_period_divides(4 * RPI), "the swizzle must repeat every instruction row step");
     base = const_cast<bf16*>(b);
     nbytes = (int)((int64_t)Tk * row_stride * 2);
     tile_bytes = (uint32_t)(kBN * row_stride * 2);
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int lin = (i * 4 + wave) * 64 + lane;
-      const int row = lin / DCH, slot = lin % DCH;
-      const int sw = tile_swz<D>(row);
-      voff[i] = (uint32_t)(((int64_t)row * row_stride + (slot ^ sw) * 8) * 2);
-    }
+    step_bytes = (uint32_t)(4 * RPI * row_stride * 2);
+    const int row = wave * RPI + lane / DCH, slot = lane % DCH;
+    voff = (uint32_t)(((int64_t)row * row_stride + (slot ^ tile_swz<D>(row)) * 8) * 2);
   }
   // The buffer-resource type exists only for the device target; the host
   // pass of this translation unit sees an empty body.
@@ -104,8 +113,8 @@ struct TileLoader {
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, nbytes, 0x00020000);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + (i * 4 + wave) * 64 * 8), 16, voff[i],
-                                               (uint32_t)t * tile_bytes, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + (i * 4 + wave) * 64 * 8), 16, voff,
+                                               (uint32_t)t * tile_bytes + i * step_bytes, 0, 0);
 #endif
   }
 };
@@ -128,9 +137,12 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   const int id = blockIdx.x;
   int bh, mblk;
   if ((BH & 7) == 0) {
-    const int xcd = id & 7, slot = id >> 3;
-    bh = (slot / nmb) * 8 + xcd;
-    mblk = nmb - 1 - slot % nmb;
+    // Blocks are dealt to the 8 XCDs round-robin; within an XCD the issue
+    // order is longest causal q-block first across all of its heads (LPT
+    // list scheduling), so the short blocks fill the tail.
+    const int xcd = id & 7, slot = id >> 3, bpx = BH >> 3;
+    bh = (slot % bpx) * 8 + xcd;
+    mblk = nmb - 1 - slot / bpx;
   } else {
     bh = id % BH;
     mblk = nmb - 1 - id / BH;
@@ -191,9 +203,9 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   // causal diagonal) mask per element; interior tiles do no mask work.
   auto compute = [&](const bf16* kl, const bf16* vl, int kb, auto edge_tag) {
     constexpr bool EDGE = decltype(edge_tag)::value;
-    f32x16 s[2];
+    f32x16 s[kMT];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < kMT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
 #pragma unroll
@@ -206,7 +218,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
     // otherwise they stay raw and the scale is folded into the exp2 FMA.
     float mx = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float x = s[mt][i];
@@ -223,7 +235,11 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
         s[mt][i] = x;
         mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // Lanes l and l^32 hold the two halves of one query's keys.
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
     const float m_l2 = MASK ? mx : mx * sl2;
     const bool need = m_l2 > b_run + kSlack;
     if (__ballot(need)) {
@@ -237,20 +253,34 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
         for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
     }
     const float nbase = b_run == -INFINITY ? 0.f : -b_run;
-    bf16x8 pb[4];
+    bf16x8 pb[kKS];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float pv = MASK ? __builtin_amdgcn_exp2f(s[mt][i] + nbase)
                               : __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
-        l_run += pv;
         pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(pv);
       }
+    // Row sum of exactly the bf16 values the PV product consumes, two per
+    // instruction.
+    {
+      const bf16x2 one = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
+      float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < kKS; ++j) {
+        const bf16x8 w = pb[j];
+        l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[0], w[1]}, one, l0, false);
+        l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[2], w[3]}, one, l1, false);
+        l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[4], w[5]}, one, l0, false);
+        l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[6], w[7]}, one, l1, false);
+      }
+      l_run += l0 + l1;
+    }
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int ks = 0; ks < kKS; ++ks) {
         // k-slots 0-3: keys ks*16 + 4*half + e; slots 4-7: the same + 8.
         const bf16* v_rows = vl + (ks * 16 + v_row) * D + v_sub;
         const s16x4 lo =
