@@ -1,13 +1,13 @@
 // Row-reduction kernels for gfx950: LayerNorm, RMSNorm and softmax over the
 // last axis.
 //
-// One row is owned by a group of LANES threads (16 or 64 lanes of one
-// wavefront, or a 256-thread workgroup).  Each lane loads NV 16-byte vectors
-// with consecutive lanes on consecutive vectors, so every load instruction of
-// a wavefront covers 1 KiB of contiguous row data.  The row stays in
-// registers: LayerNorm is two-pass (mean, then sum of squared deviations)
-// without re-reading HBM, so each element is read once and written once —
-// the HBM roofline's algorithmic traffic.
+// A row is owned by 16 or 64 lanes of one wavefront (rows up to 1024
+// 16-byte vectors, i.e. 4096 f32 / 8192 bf16 elements) or by a 256-thread
+// workgroup (up to 4096 vectors); longer or unaligned rows take a looped
+// fallback.  Each element is read from HBM once and written once -- the HBM
+// roofline's algorithmic traffic.
+#include <type_traits>
+
 #include "common.h"
 
 namespace mfx {
@@ -70,8 +70,28 @@ __device__ __forceinline__ float load_param(const void* p, int dt, int i) {
   return static_cast<float>(static_cast<const bf16*>(p)[i]);
 }
 
-// Sum / max over the LANES threads that own a row.  For LANES == kBlock the
-// partials of the four wavefronts meet in LDS.
+// VEC consecutive parameters of storage type PT starting at element e, as
+// fp32, in 16-byte (f32) or 8/16-byte (bf16) vector loads.
+template <typename PT, int VEC>
+__device__ __forceinline__ void load_params(const void* p, int e, float* out) {
+  if constexpr (std::is_same<PT, float>::value) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + e);
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) {
+      const float4 v = q[j];
+      out[4 * j] = v.x; out[4 * j + 1] = v.y; out[4 * j + 2] = v.z; out[4 * j + 3] = v.w;
+    }
+  } else if constexpr (VEC == 8) {
+    unpack16<bf16>(*reinterpret_cast<const uint4*>(static_cast<const bf16*>(p) + e), out);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const bf16*>(p) + e);
+    out[0] = __uint_as_float(v.x << 16); out[1] = __uint_as_float(v.x & 0xffff0000u);
+    out[2] = __uint_as_float(v.y << 16); out[3] = __uint_as_float(v.y & 0xffff0000u);
+  }
+}
+
+// Sum / max over the LANES threads that own a row.  For LANES > 64 the
+// partials of the wavefronts meet in LDS.
 template <int LANES, bool kMax>
 __device__ __forceinline__ float row_reduce(float v, float* lds) {
   if constexpr (LANES <= 64) {
@@ -89,14 +109,23 @@ __device__ __forceinline__ float row_reduce(float v, float* lds) {
   }
 }
 
-template <typename T, int LANES, int NV, RowOp OP>
+// One row per LANES threads (16 or 64 lanes of one wavefront, or a whole
+// 256-thread workgroup).  Each lane loads NV 16-byte vectors with consecutive
+// lanes on consecutive vectors, so every load instruction of a wavefront
+// covers 1 KiB of contiguous row data, and all of a row's loads are in flight
+// before the first reduction.  The gamma / beta slices a lane needs are
+// loaded as vectors of their storage type PT right after the row (L2 hits
+// after the first rows), so the epilogue is pure FMA work.  The row stays in
+// registers: LayerNorm is two-pass (mean, then sum of squared deviations)
+// without re-reading HBM, so each element is read once and written once.
+template <typename T, typename PT, int LANES, int NV, RowOp OP>
 __global__ __launch_bounds__(kBlock) void row_kernel(
     const T* __restrict__ x, T* __restrict__ y, const void* __restrict__ gamma,
-    const void* __restrict__ beta, int pdt, int64_t rows, int n, int64_t xs,
-    int64_t ys, float eps) {
+    const void* __restrict__ beta, int64_t rows, int n, int64_t xs, int64_t ys, float eps) {
   constexpr int VEC = Vec16<T>::N;
   typedef typename Vec16<T>::type V;
   constexpr int ROWS_PER_BLOCK = kBlock / LANES;
+  constexpr bool kParams = OP != RowOp::kSoftmax;
   __shared__ float lds[kBlock / 64];
 
   const int lane = threadIdx.x % LANES;
@@ -114,6 +143,23 @@ __global__ __launch_bounds__(kBlock) void row_kernel(
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[i][j] = (OP == RowOp::kSoftmax) ? -INFINITY : 0.f;
+    }
+  }
+  float gv[kParams ? NV : 1][VEC], bv[kParams && OP == RowOp::kLayerNorm ? NV : 1][VEC];
+  if constexpr (kParams) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int vi = min(i * LANES + lane, nvec - 1);
+      if (gamma) load_params<PT, VEC>(gamma, vi * VEC, gv[i]);
+      else
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) gv[i][j] = 1.f;
+      if constexpr (OP == RowOp::kLayerNorm) {
+        if (beta) load_params<PT, VEC>(beta, vi * VEC, bv[i]);
+        else
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) bv[i][j] = 0.f;
+      }
     }
   }
 
@@ -175,16 +221,13 @@ __global__ __launch_bounds__(kBlock) void row_kernel(
     float o[VEC];
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
-      const int e = vi * VEC + j;
-      float t;
       if constexpr (OP == RowOp::kSoftmax) {
-        t = v[i][j] * scale_or_max;
+        o[j] = v[i][j] * scale_or_max;
+      } else if constexpr (OP == RowOp::kLayerNorm) {
+        o[j] = fmaf((v[i][j] - shift) * scale_or_max, gv[i][j], bv[i][j]);
       } else {
-        t = (v[i][j] - shift) * scale_or_max;
-        if (gamma) t *= load_param(gamma, pdt, e);
-        if (OP == RowOp::kLayerNorm && beta) t += load_param(beta, pdt, e);
+        o[j] = v[i][j] * scale_or_max * gv[i][j];
       }
-      o[j] = t;
     }
     yr[vi] = pack16<T>(o);
   }
@@ -244,33 +287,44 @@ __global__ __launch_bounds__(kBlock) void row_kernel_looped(
   }
 }
 
-template <typename T, int LANES, int NV, RowOp OP>
+template <typename T, typename PT, int LANES, int NV, RowOp OP>
 int launch_rows(const mfx_norm_args& a, hipStream_t s) {
   constexpr int rpb = kBlock / LANES;
   const int64_t blocks = (a.rows + rpb - 1) / rpb;
-  hipLaunchKernelGGL((row_kernel<T, LANES, NV, OP>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
-                     static_cast<const T*>(a.x), static_cast<T*>(a.y), a.gamma, a.beta,
-                     a.param_dtype, a.rows, (int)a.n, a.x_row_stride, a.y_row_stride, a.eps);
+  hipLaunchKernelGGL((row_kernel<T, PT, LANES, NV, OP>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                     static_cast<const T*>(a.x), static_cast<T*>(a.y), a.gamma, a.beta, a.rows, (int)a.n,
+                     a.x_row_stride, a.y_row_stride, a.eps);
   return launch_status("row_kernel");
+}
+
+template <typename T, typename PT, RowOp OP>
+int dispatch_vec(const mfx_norm_args& a, hipStream_t s, int64_t nvec) {
+  if (nvec <= 16) return launch_rows<T, PT, 16, 1, OP>(a, s);
+  if (nvec <= 32) return launch_rows<T, PT, 16, 2, OP>(a, s);
+  if (nvec <= 64) return launch_rows<T, PT, 16, 4, OP>(a, s);
+  if (nvec <= 128) return launch_rows<T, PT, 64, 2, OP>(a, s);
+  if (nvec <= 256) return launch_rows<T, PT, 64, 4, OP>(a, s);
+  if (nvec <= 512) return launch_rows<T, PT, 64, 8, OP>(a, s);
+  if (nvec <= 1024) return launch_rows<T, PT, 64, 16, OP>(a, s);
+  if (nvec <= 2048) return launch_rows<T, PT, 256, 8, OP>(a, s);
+  return launch_rows<T, PT, 256, 16, OP>(a, s);
 }
 
 template <typename T, RowOp OP>
 int dispatch_typed(const mfx_norm_args& a, hipStream_t s) {
   constexpr int VEC = Vec16<T>::N;
+  const bool params = OP != RowOp::kSoftmax && (a.gamma || (OP == RowOp::kLayerNorm && a.beta));
+  // Parameter vectors are read at element offsets that are multiples of VEC.
+  const int pbytes = a.param_dtype == MFX_F32 ? 4 : 2;
+  const bool params_aligned = !params || ((!a.gamma || (uintptr_t)a.gamma % (VEC * pbytes > 16 ? 16 : VEC * pbytes) == 0) &&
+                                          (!a.beta || (uintptr_t)a.beta % (VEC * pbytes > 16 ? 16 : VEC * pbytes) == 0));
   const bool aligned = (a.n % VEC == 0) && (a.x_row_stride % VEC == 0) &&
                        (a.y_row_stride % VEC == 0) &&
-                       ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.y % 16 == 0);
+                       ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.y % 16 == 0) && params_aligned;
   const int64_t nvec = a.n / VEC;
-  if (aligned) {
-    if (nvec <= 16) return launch_rows<T, 16, 1, OP>(a, s);
-    if (nvec <= 32) return launch_rows<T, 16, 2, OP>(a, s);
-    if (nvec <= 64) return launch_rows<T, 16, 4, OP>(a, s);
-    if (nvec <= 128) return launch_rows<T, 64, 2, OP>(a, s);
-    if (nvec <= 256) return launch_rows<T, 64, 4, OP>(a, s);
-    if (nvec <= 512) return launch_rows<T, 64, 8, OP>(a, s);
-    if (nvec <= 1024) return launch_rows<T, 256, 4, OP>(a, s);
-    if (nvec <= 2048) return launch_rows<T, 256, 8, OP>(a, s);
-    if (nvec <= 4096) return launch_rows<T, 256, 16, OP>(a, s);
+  if (aligned && nvec <= 4096) {
+    if (params && a.param_dtype == MFX_BF16) return dispatch_vec<T, bf16, OP>(a, s, nvec);
+    return dispatch_vec<T, float, OP>(a, s, nvec);
   }
   hipLaunchKernelGGL((row_kernel_looped<T, OP>), dim3((unsigned)a.rows), dim3(kBlock), 0, s,
                      static_cast<const T*>(a.x), static_cast<T*>(a.y), a.gamma, a.beta,
