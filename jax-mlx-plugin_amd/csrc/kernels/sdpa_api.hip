@@ -7,7 +7,7 @@
 namespace mfx {
 namespace {
 
-enum class Kind { kFlashBf16, kFlashF32, kDecode, kGeneric };
+enum class Kind { kFlashBf16, kFlashF32, kDecode, kDecodeMfma, kGeneric };
 
 struct Plan {
   SdpaParams p{};
@@ -63,6 +63,24 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
   p.num_splits = 1;
   p.split_len = p.Tk;
 
+  if (p.Tq <= 4 && decode_mfma_supports(p)) {
+    // One wavefront per (batch, kv head, split); enough splits to give the
+    // CUs several waves each, each split a whole number of 64-key tiles.
+    out.kind = Kind::kDecodeMfma;
+    const int pairs = p.B * p.Hkv;
+    const int tile = decode_mfma_tile();
+    const int tiles = (p.Tk + tile - 1) / tile;
+    int splits = (4096 + pairs - 1) / pairs;
+    splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
+    int len = (tiles + splits - 1) / splits * tile;
+    if (len > decode_mfma_max_split_len()) len = decode_mfma_max_split_len();
+    splits = (p.Tk + len - 1) / len;
+    p.num_splits = splits;
+    p.split_len = len;
+    if (splits > 1)
+      out.partial_bytes = (size_t)splits * p.B * p.Hq * p.Tq * (p.Dv + 2) * sizeof(float);
+    return MFX_OK;
+  }
   if (p.Tq <= 4 && decode_supports(p)) {
     out.kind = Kind::kDecode;
     const int pairs = p.B * p.Hkv;
@@ -94,6 +112,7 @@ const char* kind_name(const Plan& pl) {
     case Kind::kFlashBf16: return pl.p.D == 128 ? "flash_bf16_d128" : "flash_bf16_d64";
     case Kind::kFlashF32: return pl.p.D == 128 ? "flash_f32_d128" : "flash_f32_d64";
     case Kind::kDecode: return "decode_splitkv";
+    case Kind::kDecodeMfma: return "decode_splitkv_mfma";
     default: return "generic";
   }
 }
@@ -178,6 +197,7 @@ int mfx_sdpa_fwd(const mfx_sdpa_args* args, void* stream) {
     case Kind::kFlashBf16: return launch_flash_bf16(p, s);
     case Kind::kFlashF32: return launch_flash_f32(p, s);
     case Kind::kDecode: return launch_decode(p, s);
+    case Kind::kDecodeMfma: return launch_decode_mfma(p, s);
     default: return launch_generic(p, s);
   }
 }

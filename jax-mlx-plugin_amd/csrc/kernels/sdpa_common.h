@@ -30,11 +30,16 @@ struct SdpaParams {
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s);
 int launch_flash_f32(const SdpaParams& p, hipStream_t s);
 int launch_decode(const SdpaParams& p, hipStream_t s);
+int launch_decode_mfma(const SdpaParams& p, hipStream_t s);
+int launch_decode_combine(const SdpaParams& p, hipStream_t s);  // merges split partials
 int launch_generic(const SdpaParams& p, hipStream_t s);
 
 bool flash_bf16_supports(const SdpaParams& p);
 bool flash_f32_supports(const SdpaParams& p);
 bool decode_supports(const SdpaParams& p);
+bool decode_mfma_supports(const SdpaParams& p);
+int decode_mfma_max_split_len();  // keys per split the MFMA decode accepts
+int decode_mfma_tile();           // split lengths are multiples of this
 
 // Loads one additive-mask element as fp32.
 __device__ __forceinline__ float load_mask(const void* m, int dt, int64_t off) {

@@ -270,9 +270,7 @@ int launch_t(const SdpaParams& p, hipStream_t s) {
   hipLaunchKernelGGL((decode_kernel<T, D, R, MASK, CAUSAL>), grid, dim3(kNT), 0, s, p);
   int rc = launch_status("decode_kernel");
   if (rc != MFX_OK || p.num_splits == 1) return rc;
-  hipLaunchKernelGGL((decode_combine_kernel<T>), dim3((unsigned)(p.B * p.Hq * p.Tq)), dim3(128), 0,
-                     s, p);
-  return launch_status("decode_combine_kernel");
+  return launch_decode_combine(p, s);
 }
 
 template <typename T, int D, int R>
@@ -304,6 +302,14 @@ bool decode_supports(const SdpaParams& p) {
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % e || p.ks[i] % e || p.vs[i] % e) return false;
   return true;
+}
+
+int launch_decode_combine(const SdpaParams& p, hipStream_t s) {
+  if (p.dtype == MFX_BF16)
+    hipLaunchKernelGGL((decode_combine_kernel<bf16>), dim3((unsigned)(p.B * p.Hq * p.Tq)), dim3(128), 0, s, p);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<float>), dim3((unsigned)(p.B * p.Hq * p.Tq)), dim3(128), 0, s, p);
+  return launch_status("decode_combine_kernel");
 }
 
 int launch_decode(const SdpaParams& p, hipStream_t s) {

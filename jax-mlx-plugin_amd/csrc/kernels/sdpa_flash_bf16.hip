@@ -31,7 +31,7 @@
 // first, which balances the causal triangle across the CUs.
 #include <type_traits>
 
-#include "sdpa_common.h"
+#include "sdpa_tiles.h"
 
 namespace mfx {
 namespace {
@@ -42,82 +42,13 @@ constexpr int kMT = kBN / 32;  // 32-key score blocks per tile
 constexpr int kKS = kBN / 16;  // 16-key PV steps per tile
 constexpr int kNT = 256;  // threads per workgroup
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
-
-// Exponent slack of the lazy rescale: the running base of a row's exp2 is
-// only raised when a new score exceeds it by more than this (log2 units), so
-// un-normalised probabilities stay below 2^8 and the O / l rescale runs a
-// handful of times per row instead of once per tile.  The result is exact:
-// O and l always share the same base.
-constexpr float kSlack = 8.0f;
-
-// 16-byte chunk c of tile row r is stored at chunk slot c ^ tile_swz<D>(r).  The
-// K operand reads (lanes on consecutive rows, one chunk each) and the
-// transposing V reads (4 rows x 2 chunks per 16 lanes) must spread over all
-// banks whether the LDS serves 128 or 256 bytes per clock: for d = 128 the
-// map is a bijection on each aligned run of 16 rows that is also one-to-one
-// on bits 0-2 for 8 rows and on bits 1-2 and 2-3 for 4 rows; d = 64 rows
-// have only 8 chunks and use a period-8 map.
+using tiles::kSlack;
+using tiles::lds_s16x4_t;
+using tiles::s16x4;
+using tiles::tile_swz;
+using tiles::wait_dma;
 template <int D>
-__host__ __device__ constexpr int tile_swz(int r) {
-  if constexpr (D == 128) return (r & 3) | (((r ^ (r >> 2)) & 3) << 2);
-  return ((r & 3) << 1) | ((r >> 2) & 1);
-}
-
-// s_waitcnt vmcnt(0), other counters left alone: this wave's LDS-DMA
-// loads have landed.
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Copies keys [kb, kb + kBN) x D of one (batch, head) into a swizzled LDS
-// tile with buffer loads to LDS.  Instruction i of wave w fills tile chunks
-// (4i + w)*64 .. +63, one 16-byte chunk per lane, i.e. rows
-// (4i + w)*RPI .. +RPI-1 with RPI = 64 / (D/8).  The swizzle repeats every
-// 4*RPI rows (16 for d = 128, 32 for d = 64; its period divides both), so
-// instruction i reads the same per-lane source offset as instruction 0 plus
-// i*4*RPI rows: one VGPR per operand, and the tile start and the step are
-// scalar offsets.  The resource spans the Tk keys of this (batch, head):
-// rows past Tk are out of range and read as zeros (their scores are masked
-// to -inf, so they contribute exactly 0).
-template <int D>
-struct TileLoader {
-  static constexpr int DCH = D / 8;
-  static constexpr int RPI = 64 / DCH;  // rows per load instruction
-  static constexpr int LOADS = kBN * DCH / kNT;
-  static constexpr bool swz_period_divides(int step) {
-    for (int r = 0; r < kBN; ++r)
-      if (tile_swz<D>(r) != tile_swz<D>(r + step)) return false;
-    return true;
-  }
-  bf16* base;
-  int nbytes;           // extent of the resource: Tk rows
-  uint32_t voff;        // per-lane source offset of instruction 0
-  uint32_t step_bytes;  // scalar offset step per instruction
-  uint32_t tile_bytes;  // scalar offset step per tile
-
-  __device__ __forceinline__ TileLoader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
-    static_assert(swz_period_divides(4 * RPI), "the swizzle must repeat every instruction row step");
-    base = const_cast<bf16*>(b);
-    nbytes = (int)((int64_t)Tk * row_stride * 2);
-    tile_bytes = (uint32_t)(kBN * row_stride * 2);
-    step_bytes = (uint32_t)(4 * RPI * row_stride * 2);
-    const int row = wave * RPI + lane / DCH, slot = lane % DCH;
-    voff = (uint32_t)(((int64_t)row * row_stride + (slot ^ tile_swz<D>(row)) * 8) * 2);
-  }
-  // The buffer-resource type exists only for the device target; the host
-  // pass of this translation unit sees an empty body.
-  __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, nbytes, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + (i * 4 + wave) * 64 * 8), 16, voff,
-                                               (uint32_t)t * tile_bytes + i * step_bytes, 0, 0);
-#endif
-  }
-};
+using TileLoader = tiles::TileLoader<D, kBN, kNT / 64>;
 
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {

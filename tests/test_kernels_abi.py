@@ -46,9 +46,15 @@ def test_kernel_selection_per_config(native):
     # config 2: f32 B8/H8/T128/d64 -> fp32 MFMA flash kernel
     q, k, v = _cpu_tensors(torch, (8, 8, 128, 64), (8, 8, 128, 64), (8, 8, 128, 64), dtype=torch.float32)
     assert native.sdpa_kernel_name(q, k, v) == "flash_f32_d64"
-    # config 5: GQA decode Hq32/Hkv8, Tq=1 -> split-KV decode
+    # config 5: GQA decode Hq32/Hkv8, Tq=1 -> split-KV decode on the matrix cores
     q, k, v = _cpu_tensors(torch, (16, 32, 1, 128), (16, 8, 8192, 128), (16, 8, 8192, 128))
-    assert native.sdpa_kernel_name(q, k, v, q_rms_eps=1e-6) == "decode_splitkv"
+    assert native.sdpa_kernel_name(q, k, v, q_rms_eps=1e-6) == "decode_splitkv_mfma"
+    # the same in f32 -> the vector-ALU split-KV decode
+    q, k, v = _cpu_tensors(torch, (2, 8, 1, 128), (2, 2, 512, 128), (2, 2, 512, 128), dtype=torch.float32)
+    assert native.sdpa_kernel_name(q, k, v) == "decode_splitkv"
+    # up to 32 query rows per kv head (8 heads x 4 positions) stay on the MFMA decode
+    q, k, v = _cpu_tensors(torch, (1, 16, 4, 64), (1, 2, 700, 64), (1, 2, 700, 64))
+    assert native.sdpa_kernel_name(q, k, v) == "decode_splitkv_mfma"
     # BTNH (JAX layout) views are accepted without a copy
     q, k, v = _cpu_tensors(torch, (2, 256, 8, 64), (2, 256, 8, 64), (2, 256, 8, 64))
     assert native.sdpa_kernel_name(q, k, v, layout="bthd") == "flash_bf16_d64"

@@ -218,7 +218,7 @@ def test_sdpa_config5_decode_rmsnorm_full_size(cuda, nat, oracle):
     lens = rng.integers(1024, 8192, size=16, endpoint=True)
     mask = np.where(np.arange(8192)[None] < lens[:, None], 0.0, -np.inf).reshape(16, 1, 1, 8192)
     maskd = dev(cuda, mask, cuda.float32)
-    assert nat.sdpa_kernel_name(q, k, v, mask=maskd, q_rms_eps=1e-6) == "decode_splitkv"
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd, q_rms_eps=1e-6) == "decode_splitkv_mfma"
     out = nat.sdpa(q, k, v, scale=128 ** -0.5, mask=maskd, q_rms_eps=1e-6)
     qn = oracle.rms_norm(host(q), None, 1e-6)
     qn = host(cuda.from_numpy(qn.astype(np.float32)).bfloat16())  # the graph's bf16 RMSNorm output
@@ -231,7 +231,7 @@ def test_sdpa_config5_decode_rmsnorm_full_size(cuda, nat, oracle):
 def test_sdpa_decode_variants(cuda, nat, oracle, dtype, hq, hkv, tq, D):
     td = cuda.float32 if dtype == "f32" else cuda.bfloat16
     q, k, v = make_qkv(cuda, 9, (3, hq, tq, D), (3, hkv, 3000, D), td)
-    assert nat.sdpa_kernel_name(q, k, v) == "decode_splitkv"
+    assert nat.sdpa_kernel_name(q, k, v) == ("decode_splitkv" if dtype == "f32" else "decode_splitkv_mfma")
     w = dev(cuda, 1 + 0.1 * np.random.default_rng(10).standard_normal(D), td)
     out = nat.sdpa(q, k, v, scale=0.1, q_rms_eps=1e-5, q_rms_weight=w)
     qn = oracle.rms_norm(host(q), host(w), 1e-5)
@@ -265,3 +265,43 @@ def test_sdpa_fully_masked_rows_are_nan(cuda, nat, tq):
     assert bool(cuda.isnan(out[:, :, 0]).all())
     if tq > 1:
         assert bool(cuda.isfinite(out[:, :, 1:]).all())
+
+
+@pytest.mark.parametrize("hq,hkv,tq,D,tk", [(32, 1, 1, 128, 64), (16, 2, 4, 64, 1000), (8, 8, 1, 128, 4097),
+                                            (32, 4, 4, 128, 777), (4, 2, 1, 64, 1)])
+def test_sdpa_decode_mfma_rows_and_ragged_splits(cuda, nat, oracle, hq, hkv, tq, D, tk):
+    """Up to 32 query rows per kv head, Tk not a multiple of the 64-key tile,
+    split boundaries, a single key; plus the causal variant (query t sees
+    keys 0..t)."""
+    q, k, v = make_qkv(cuda, 21, (2, hq, tq, D), (2, hkv, tk, D), cuda.bfloat16)
+    assert nat.sdpa_kernel_name(q, k, v) == "decode_splitkv_mfma"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5), "bf16")
+    out_c = nat.sdpa(q, k, v, scale=D ** -0.5, causal=True)
+    check_sdpa(out_c, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=True), "bf16")
+
+
+def test_sdpa_decode_mfma_per_row_mask_and_holes(cuda, nat, oracle):
+    """An additive mask that differs per head and per query position, with
+    holes (-inf runs inside the valid range) and finite biases; one batch has
+    a fully masked 64-key tile run that the prepass must skip."""
+    rng = np.random.default_rng(22)
+    B, Hq, Hkv, Tq, S, D = 2, 8, 2, 2, 900, 128
+    q, k, v = make_qkv(cuda, 23, (B, Hq, Tq, D), (B, Hkv, S, D), cuda.bfloat16)
+    mask = rng.standard_normal((B, Hq, Tq, S)) * 0.5
+    mask[:, :, :, 100:300] = -np.inf                 # whole tiles masked for every row
+    mask[0, 3, 1, 500:900] = -np.inf                 # one row sees a shorter prefix
+    mask[1, :, 0, ::7] = -np.inf                     # holes
+    maskd = dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd) == "decode_splitkv_mfma"
+    out = nat.sdpa(q, k, v, scale=0.09, mask=maskd)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 0.09, mask=mask), "bf16")
+
+
+def test_sdpa_decode_mfma_fully_masked_row_is_nan(cuda, nat):
+    q, k, v = make_qkv(cuda, 24, (1, 4, 1, 64), (1, 2, 300, 64), cuda.bfloat16)
+    mask = cuda.zeros(1, 4, 1, 300, device="cuda")
+    mask[:, 1] = float("-inf")
+    out = nat.sdpa(q, k, v, scale=0.125, mask=mask).float()
+    assert bool(cuda.isnan(out[:, 1]).all())
+    assert bool(cuda.isfinite(out[:, [0, 2, 3]]).all())
