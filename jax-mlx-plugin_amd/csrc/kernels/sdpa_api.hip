@@ -64,19 +64,21 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
   p.split_len = p.Tk;
 
   if (p.Tq <= 4 && decode_mfma_supports(p)) {
-    // One wavefront per (batch, kv head, split); enough splits to give the
-    // CUs several waves each, each split a whole number of 64-key tiles.
+    // W wavefronts per (batch, kv head), wavefront j owning tiles j, j+W, ...:
+    // at most 1024 wavefronts in all (four 32 KB-LDS workgroups per CU, the
+    // whole grid resident at once, so no second round forms a tail), at
+    // least two tiles each, at most the tile bitmap's width each.
     out.kind = Kind::kDecodeMfma;
     const int pairs = p.B * p.Hkv;
-    const int tile = decode_mfma_tile();
-    const int tiles = (p.Tk + tile - 1) / tile;
-    int splits = (4096 + pairs - 1) / pairs;
-    splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
-    int len = (tiles + splits - 1) / splits * tile;
-    if (len > decode_mfma_max_split_len()) len = decode_mfma_max_split_len();
-    splits = (p.Tk + len - 1) / len;
+    const int tiles = (p.Tk + decode_mfma_tile() - 1) / decode_mfma_tile();
+    int w = 1024 / pairs;
+    if (w > (tiles + 1) / 2) w = (tiles + 1) / 2;
+    const int wmin = (tiles + decode_mfma_max_tiles() - 1) / decode_mfma_max_tiles();
+    if (w < wmin) w = wmin;
+    if (w < 1) w = 1;
+    const int splits = w;
     p.num_splits = splits;
-    p.split_len = len;
+    p.split_len = 0;
     if (splits > 1)
       out.partial_bytes = (size_t)splits * p.B * p.Hq * p.Tq * (p.Dv + 2) * sizeof(float);
     return MFX_OK;

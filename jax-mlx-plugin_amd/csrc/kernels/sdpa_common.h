@@ -22,8 +22,8 @@ struct SdpaParams {
   int causal;
   float scale_log2;  // scale * log2(e)
   float q_rms_eps;   // < 0: no RMSNorm on q
-  int num_splits;    // split-KV decode only
-  int split_len;     // keys per split
+  int num_splits;    // split-KV decode only: partials per row
+  int split_len;     // keys per split (VALU decode; the MFMA decode interleaves tiles)
 };
 
 // Kernel families; each returns MFX_OK or an error code after launching.
@@ -38,8 +38,8 @@ bool flash_bf16_supports(const SdpaParams& p);
 bool flash_f32_supports(const SdpaParams& p);
 bool decode_supports(const SdpaParams& p);
 bool decode_mfma_supports(const SdpaParams& p);
-int decode_mfma_max_split_len();  // keys per split the MFMA decode accepts
-int decode_mfma_tile();           // split lengths are multiples of this
+int decode_mfma_tile();       // keys per tile of the MFMA decode
+int decode_mfma_max_tiles();  // tiles one of its wavefronts can own
 
 // Loads one additive-mask element as fp32.
 __device__ __forceinline__ float load_mask(const void* m, int dt, int64_t off) {

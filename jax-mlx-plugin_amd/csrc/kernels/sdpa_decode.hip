@@ -236,32 +236,58 @@ __global__ __launch_bounds__(kNT) void decode_kernel(SdpaParams p) {
   }
 }
 
+// Merges the split partials (m, l, O) of one output row per wavefront: lane
+// s holds split s's (m, l) (64 splits per pass), the base and the weights
+// come from two wave reductions, and each lane then sums its D/64 output
+// columns over the splits with the weights broadcast from their lanes.
 template <typename T>
-__global__ __launch_bounds__(128) void decode_combine_kernel(SdpaParams p) {
-  const int64_t row = blockIdx.x;  // (b*Hq + h)*Tq + t
-  const int D = p.Dv;
-  const int rows_total = p.B * p.Hq * p.Tq;
+__global__ __launch_bounds__(256) void decode_combine_kernel(SdpaParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*Hq + h)*Tq + t
+  const int64_t rows_total = (int64_t)p.B * p.Hq * p.Tq;
+  if (row >= rows_total) return;
+  const int D = p.Dv, S = p.num_splits;
+  const int64_t stride = rows_total * (D + 2);
+  const float* base = p.partial + row * (D + 2);
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < S; s0 += 64)
+    if (s0 + lane < S) M = fmaxf(M, base[(s0 + lane) * stride]);
+  M = group_max<64>(M);
+  const float bse = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  for (int s0 = 0; s0 < S; s0 += 64)
+    if (s0 + lane < S) L += __builtin_amdgcn_exp2f(base[(s0 + lane) * stride] - bse) * base[(s0 + lane) * stride + 1];
+  L = group_sum<64>(L);
   const int t = (int)(row % p.Tq);
   const int bh = (int)(row / p.Tq);
   const int b = bh / p.Hq, h = bh % p.Hq;
-  float M = -INFINITY;
-  for (int s = 0; s < p.num_splits; ++s)
-    M = fmaxf(M, p.partial[((int64_t)s * rows_total + row) * (D + 2)]);
-  const float bse = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  for (int s = 0; s < p.num_splits; ++s) {
-    const float* part = p.partial + ((int64_t)s * rows_total + row) * (D + 2);
-    L += __builtin_amdgcn_exp2f(part[0] - bse) * part[1];
-  }
   T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + t * p.os[2];
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float O = 0.f;
-    for (int s = 0; s < p.num_splits; ++s) {
-      const float* part = p.partial + ((int64_t)s * rows_total + row) * (D + 2);
-      O += __builtin_amdgcn_exp2f(part[0] - bse) * part[2 + d];
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // columns lane, lane+64, ... (D <= 256)
+  const int nc = (D + 63) / 64;
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    const float w = s0 + lane < S ? __builtin_amdgcn_exp2f(base[(s0 + lane) * stride] - bse) : 0.f;
+    const int n = min(64, S - s0);
+    // Sixteen splits per batch: their loads are independent and issued
+    // together, so a row costs a few L2 round trips, not one per split.
+    for (int j0 = 0; j0 < n; j0 += 16) {
+      float ov[16][4];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          ov[j][c] = (j0 + j < n && c < nc && c * 64 + lane < D) ? base[(s0 + j0 + j) * stride + 2 + c * 64 + lane] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float wj = __shfl(w, min(j0 + j, 63), 64);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += wj * ov[j][c];
+      }
     }
-    orow[d] = from_f32<T>(O / L);
   }
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (c * 64 + lane < D) orow[c * 64 + lane] = from_f32<T>(acc[c] * inv);
 }
 
 template <typename T, int D, int R, bool MASK, bool CAUSAL>
@@ -305,10 +331,11 @@ bool decode_supports(const SdpaParams& p) {
 }
 
 int launch_decode_combine(const SdpaParams& p, hipStream_t s) {
+  const unsigned blocks = (unsigned)(((int64_t)p.B * p.Hq * p.Tq + 3) / 4);
   if (p.dtype == MFX_BF16)
-    hipLaunchKernelGGL((decode_combine_kernel<bf16>), dim3((unsigned)(p.B * p.Hq * p.Tq)), dim3(128), 0, s, p);
+    hipLaunchKernelGGL((decode_combine_kernel<bf16>), dim3(blocks), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((decode_combine_kernel<float>), dim3((unsigned)(p.B * p.Hq * p.Tq)), dim3(128), 0, s, p);
+    hipLaunchKernelGGL((decode_combine_kernel<float>), dim3(blocks), dim3(256), 0, s, p);
   return launch_status("decode_combine_kernel");
 }
 

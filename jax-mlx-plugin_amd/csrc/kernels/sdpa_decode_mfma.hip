@@ -3,8 +3,10 @@
 //
 // The R = (Hq/Hkv) * Tq query rows that share one kv head (R <= 32) are the
 // columns of one 32-wide MFMA operand, so every K/V row is read from HBM once
-// for all of them.  The grid is (splits, B*Hkv); one wavefront per workgroup
-// walks the keys of its split in 64-key tiles:
+// for all of them.  The grid is (B*Hkv, W): W wavefronts (one per workgroup)
+// share a kv head and wavefront j takes the 32-key tiles j, j+W, j+2W, ...,
+// so every wavefront gets an equal share of a valid prefix (a length-masked
+// cache) and the partial results of the W wavefronts merge at the end:
 //   S^T = K Q^T   A = K tile rows (LDS), B = the R query rows (registers,
 //                 zero-padded to 32 columns): v_mfma_f32_32x32x16_bf16.
 //   O^T = V^T P^T A = transposing LDS reads of the V tile, B = P straight
@@ -16,9 +18,9 @@
 // K/V tiles stream through two swizzled LDS stages by asynchronous LDS-DMA
 // loads; while one tile is computed, the next valid tile is in flight.  A
 // prepass marks the tiles that hold at least one visible key (additive mask
-// not -inf for some row, key < end of split, causal limit), and only those
-// are loaded, so a padded KV cache costs the bytes of its valid prefix.
-// The split partials (m, l, O) merge in the split-KV combine kernel.
+// not -inf for some row, key < Tk, causal limit), and only those are
+// loaded, so a padded KV cache costs the bytes of its valid prefix.  The W
+// partials (m, l, O) of a row merge in the split-KV combine kernel.
 //
 // Optional fused RMSNorm of the query rows (reference chain rms_norm -> sdpa
 // of GQA decode): q is normalised in fp32 and rounded to bf16 before it is
@@ -38,8 +40,7 @@ using tiles::tile_swz;
 constexpr int kDN = 32;  // keys per tile: 32 KB of LDS per workgroup, five per CU
 constexpr int kMT = kDN / 32;
 constexpr int kKS = kDN / 16;
-constexpr int kMaxTiles = 64;  // per split: width of the valid-tile bitmap
-constexpr int kPrepassKeys = 64;  // keys per prepass load (one per lane)
+constexpr int kMaxTiles = 64;  // per wavefront: width of the valid-tile bitmap
 
 // s_waitcnt vmcnt(N) with the other counters left alone (N < 64).
 template <int N>
@@ -58,7 +59,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 
   const int lane = threadIdx.x;
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x, bhk = blockIdx.y;
+  const int split = blockIdx.y, bhk = blockIdx.x;  // split = this wavefront's tile phase j
+  const int W = p.num_splits;
   const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
   const int Tq = p.Tq, R = p.group * Tq, Tk = p.Tk;
 
@@ -102,49 +104,48 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   }
   const float sl2 = p.scale_log2;  // > 0 (checked on the host)
 
-  const int kbeg = split * p.split_len;
-  const int kend = min(Tk, kbeg + p.split_len);
-  const int ntile = kend > kbeg ? (kend - kbeg + kDN - 1) / kDN : 0;
+  // This wavefront's tiles: global tile split + W*i, i = 0 .. ntile-1.
+  const int tiles_total = (Tk + kDN - 1) / kDN;
+  const int ntile = split < tiles_total ? (tiles_total - split + W - 1) / W : 0;  // <= kMaxTiles (host)
   int64_t m_base = 0;
   if constexpr (MASK) m_base = b * p.ms[0] + hq * p.ms[1] + tq * p.ms[2];
 
-  // Prepass: bit t set when tile t holds a key some row can see.  Lane l
-  // checks key kbeg + 64c + l of chunk c; a chunk covers 64/kDN tiles.  The
-  // chunks' loads are issued eight at a time, so a split costs one or two
-  // round trips.  A mask that does not vary over heads and query positions
-  // is checked once per key, otherwise once per (row, key).
+  // Prepass: bit i set when local tile i holds a key some row can see.  Lane
+  // l checks key (l % 32) of local tile 2c + l/32; the loads of all chunks
+  // are issued eight at a time, so the whole prepass costs one or two round
+  // trips.  A mask that does not vary over heads and query positions is
+  // checked once per key, otherwise once per (row, key).
   uint64_t vbits = 0;
   {
     const bool bcast = !MASK || ((p.ms[1] == 0 || p.group == 1) && (p.ms[2] == 0 || Tq == 1));
-    const int nchunk = (kend - kbeg + kPrepassKeys - 1) / kPrepassKeys;
+    const int nchunk = (ntile + 1) / 2;
     for (int c0 = 0; c0 < nchunk; c0 += 8) {
       bool ok[8];
+      int keyj[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int key = kbeg + (c0 + j) * kPrepassKeys + lane;
-        ok[j] = c0 + j < nchunk && key < kend;
+        const int i = 2 * (c0 + j) + (lane >> 5);
+        const int key = (split + W * i) * kDN + (lane & 31);
+        keyj[j] = min(key, Tk - 1);
+        ok[j] = i < ntile && key < Tk;
         if (CAUSAL) ok[j] = ok[j] && key <= Tq - 1;
       }
       if constexpr (MASK) {
         if (bcast) {
           float mvv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int key = min(kbeg + (c0 + j) * kPrepassKeys + lane, Tk - 1);
-            mvv[j] = load_mask(p.mask, p.mask_dtype, b * p.ms[0] + (int64_t)key * p.ms[3]);
-          }
+          for (int j = 0; j < 8; ++j) mvv[j] = load_mask(p.mask, p.mask_dtype, b * p.ms[0] + (int64_t)keyj[j] * p.ms[3]);
 #pragma unroll
           for (int j = 0; j < 8; ++j) ok[j] = ok[j] && mvv[j] != -INFINITY;
         } else {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const int key = min(kbeg + (c0 + j) * kPrepassKeys + lane, Tk - 1);
             bool any = false;
             for (int r = 0; r < R; ++r) {
               const int h2 = hk * p.group + r / Tq, t2 = r % Tq;
               const float mvv = load_mask(p.mask, p.mask_dtype,
-                                          b * p.ms[0] + h2 * p.ms[1] + t2 * p.ms[2] + (int64_t)key * p.ms[3]);
-              any |= mvv != -INFINITY && (!CAUSAL || key <= t2);
+                                          b * p.ms[0] + h2 * p.ms[1] + t2 * p.ms[2] + (int64_t)keyj[j] * p.ms[3]);
+              any |= mvv != -INFINITY && (!CAUSAL || keyj[j] <= t2);
             }
             ok[j] = ok[j] && any;
           }
@@ -153,20 +154,17 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint64_t bal = __ballot(ok[j]);
-        constexpr int TPC = kPrepassKeys / kDN;  // tiles per chunk
-#pragma unroll
-        for (int u = 0; u < TPC; ++u) {
-          const uint64_t part = (bal >> (u * kDN)) & ((kDN == 64) ? ~0ull : ((1ull << kDN) - 1));
-          const int tile = (c0 + j) * TPC + u;
-          if (part && tile < kMaxTiles) vbits |= 1ull << tile;
-        }
+        const int i = 2 * (c0 + j);
+        if ((bal & 0xffffffffull) && i < kMaxTiles) vbits |= 1ull << i;
+        if ((bal >> 32) && i + 1 < kMaxTiles) vbits |= 1ull << (i + 1);
       }
     }
   }
 
-  const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1] + (int64_t)kbeg * p.ks[2];
-  const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1] + (int64_t)kbeg * p.vs[2];
-  const Loader kload(kp, p.ks[2], Tk - kbeg, 0, lane), vload(vp, p.vs[2], Tk - kbeg, 0, lane);
+  const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+  const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+  const Loader kload(kp, p.ks[2], Tk, 0, lane), vload(vp, p.vs[2], Tk, 0, lane);
+  auto gtile = [&](int i) { return split + W * i; };
 
   f32x16 o[D / 32];
 #pragma unroll
@@ -196,10 +194,10 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   }
 
   // Mask values of tile tn in the S^T lane layout (keys past Tk clamped:
-  // they are masked by the key < kend test).
+  // they are masked by the key < Tk test).
   float mv_next[kMT][16];
   auto load_tile_mask = [&](int tn) __attribute__((always_inline)) {
-    const int kb = kbeg + tn * kDN;
+    const int kb = gtile(tn) * kDN;
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
@@ -220,7 +218,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   // reads wait for the next tile's loads.
   auto body = [&](int t, int tn, const bf16* __restrict__ kc, const bf16* __restrict__ vc, bf16* __restrict__ kn,
                   bf16* __restrict__ vn) __attribute__((always_inline)) {
-    const int kb = kbeg + t * kDN;
+    const int kb = gtile(t) * kDN;
     // This tile's mask values arrived with its K/V; the next tile's are
     // issued after its DMA, so one in-order vmcnt wait covers this tile.
     float mv[kMT][16];
@@ -231,8 +229,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         for (int i = 0; i < 16; ++i) mv[mt][i] = mv_next[mt][i];
     }
     if (tn >= 0) {
-      kload.load(tn, kn, 0);
-      vload.load(tn, vn, 0);
+      kload.load(gtile(tn), kn, 0);
+      vload.load(gtile(tn), vn, 0);
       if constexpr (MASK) {
         load_tile_mask(tn);
         wait_vm<2 * Loader::LOADS + 16 * kMT>();
@@ -262,7 +260,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
         float x = s[mt][i] * sl2;
         if constexpr (MASK) x += mv[mt][i];
-        if (key >= kend || (CAUSAL && key > tq)) x = -INFINITY;
+        if (key >= Tk || (CAUSAL && key > tq)) x = -INFINITY;
         s[mt][i] = x;
         mx = fmaxf(mx, x);
       }
@@ -315,8 +313,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 
   int t = vbits ? __builtin_ctzll(vbits) : -1;
   if (t >= 0) {
-    kload.load(t, k0, 0);
-    vload.load(t, v0, 0);
+    kload.load(gtile(t), k0, 0);
+    vload.load(gtile(t), v0, 0);
     if constexpr (MASK) load_tile_mask(t);
   }
   // Two tiles per iteration (stage 0, stage 1), at most kMaxTiles tiles.
@@ -365,7 +363,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 
 template <int D, bool MASK, bool CAUSAL>
 int launch_t(const SdpaParams& p, hipStream_t s) {
-  dim3 grid((unsigned)p.num_splits, (unsigned)(p.B * p.Hkv));
+  dim3 grid((unsigned)(p.B * p.Hkv), (unsigned)p.num_splits);  // (kv heads, W)
   hipLaunchKernelGGL((decode_mfma_kernel<D, MASK, CAUSAL>), grid, dim3(64), 0, s, p);
   int rc = launch_status("decode_mfma_kernel");
   if (rc != MFX_OK || p.num_splits == 1) return rc;
@@ -388,6 +386,7 @@ bool decode_mfma_supports(const SdpaParams& p) {
   if (!(p.scale_log2 > 0.f)) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (p.group * p.Tq > 32) return false;
+  if ((int64_t)(p.Tk + kMaxTiles * kDN - 1) / (kMaxTiles * kDN) > 65535) return false;  // grid y = W
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v)) return false;
   for (int i = 0; i < 3; ++i)
@@ -396,8 +395,8 @@ bool decode_mfma_supports(const SdpaParams& p) {
   return true;
 }
 
-int decode_mfma_max_split_len() { return kMaxTiles * kDN; }
 int decode_mfma_tile() { return kDN; }
+int decode_mfma_max_tiles() { return kMaxTiles; }
 
 int launch_decode_mfma(const SdpaParams& p, hipStream_t s) {
   return p.D == 128 ? launch_d<128>(p, s) : launch_d<64>(p, s);
