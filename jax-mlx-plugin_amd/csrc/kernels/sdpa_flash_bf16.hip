@@ -135,6 +135,10 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   auto compute = [&](const bf16* kl, const bf16* vl, int kb, auto edge_tag) {
     constexpr bool EDGE = decltype(edge_tag)::value;
     f32x16 s[kMT];
+    // The two waves of a SIMD alternate between MFMA blocks and softmax
+    // work; raising a wave's priority for its MFMA blocks lets the arbiter
+    // keep the matrix core fed while the other wave's vector work fills in.
+    __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt) {
 #pragma unroll
@@ -145,6 +149,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
         s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[mt], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // MASK: scores move to the log2 domain here (scale and mask folded);
     // otherwise they stay raw and the scale is folded into the exp2 FMA.
     float mx = -INFINITY;
@@ -208,6 +213,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
       }
       l_run += l0 + l1;
     }
+    __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll

@@ -145,10 +145,7 @@ class Planner {
       if (classify(n) != Cls::kOther) continue;
       for (int v : operand_needs(n)) need_[v] = 1;
     }
-    for (const Node& n : f_.nodes)
-      if (classify(n) == Cls::kArith)
-        for (int v : n.out)
-          if (uses_[v] > 1) need_[v] = 1;
+    mark_shared_values();
     // Programs may discover more values that must be materialised: iterate.
     for (int round = 0;; ++round) {
       if (round > 4 * nvals_ + 8) throw ParseError("planner did not converge");
@@ -239,6 +236,47 @@ class Planner {
   }
 
   // Values an Other node reads from memory directly (after view tracing).
+  // A multi-use arithmetic value needs its own buffer only when the
+  // expression trees of two different programs reach it; uses inside one
+  // tree share one interpreter register through the builder's memo.  Marking
+  // a value changes the trees, so iterate to a fixed point.
+  void mark_shared_values() {
+    auto inner = [&](int u) {
+      const Node* d = def(u);
+      return d && !need_[u] && classify(*d) != Cls::kOther;
+    };
+    for (int round = 0; round < 4 * nvals_ + 8; ++round) {
+      std::vector<int> owner(nvals_, -1);  // root reaching it; -2: several roots
+      for (int r = 0; r < nvals_; ++r) {
+        const Node* dr = def(r);
+        if (!need_[r] || !dr || classify(*dr) == Cls::kOther) continue;
+        std::vector<int> stack(dr->in.begin(), dr->in.end());
+        while (!stack.empty()) {
+          const int u = stack.back();
+          stack.pop_back();
+          if (!inner(u) || owner[u] == r) continue;
+          if (owner[u] == -2) continue;
+          if (owner[u] >= 0) {
+            owner[u] = -2;
+            continue;
+          }
+          owner[u] = r;
+          for (int w : def(u)->in) stack.push_back(w);
+        }
+      }
+      bool changed = false;
+      for (const Node& n : f_.nodes) {
+        if (classify(n) != Cls::kArith) continue;
+        for (int v : n.out)
+          if (uses_[v] > 1 && !need_[v] && owner[v] == -2) {
+            need_[v] = 1;
+            changed = true;
+          }
+      }
+      if (!changed) return;
+    }
+  }
+
   std::vector<int> operand_needs(const Node& n) {
     std::vector<int> r;
     if (n.op == "stablehlo.dot_general" || n.op == "stablehlo.dot" || n.op == "stablehlo.reduce") {
