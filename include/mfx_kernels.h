@@ -88,6 +88,46 @@ int mfx_rms_norm(const mfx_norm_args* args, void* stream);
 int mfx_softmax(const mfx_norm_args* args, void* stream);
 
 /*
+ * LayerNorm backward over the last axis of [rows, n] views (feature stride 1,
+ * one row stride per tensor), for y = (x - mean) / sqrt(var + eps) * gamma + b
+ * with the population variance:
+ *   dx     = (dxh - mean(dxh) - xhat * mean(dxh * xhat)) / sqrt(var + eps),
+ *            xhat = (x - mean) / sqrt(var + eps), dxh = dy * gamma;
+ *   dgamma = sum over rows of dy * xhat;  dbeta = sum over rows of dy.
+ * gamma NULL means gamma = 1; dgamma / dbeta NULL skip that output.  x, dy and
+ * dx have `dtype`; gamma, dgamma and dbeta have `param_dtype`.  Sums run in
+ * fp32.  The parameter sums go through a workspace of
+ * mfx_layer_norm_bwd_workspace_size() bytes (NULL: library scratch).
+ * Replaces mx::vjp of fast::layer_norm behind custom_call
+ * @mlx_layer_norm_bwd (reference src/jax_mlx_pjrt.cpp:8237-8281; closed form
+ * src/jax_mlx/layer_norm.py:59-76).
+ */
+typedef struct {
+  const void* x;
+  const void* gamma;
+  const void* dy;
+  void* dx;
+  void* dgamma;
+  void* dbeta;
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t rows;
+  int64_t n;
+  int64_t x_row_stride;
+  int64_t dy_row_stride;
+  int64_t dx_row_stride;
+  float eps;
+  int32_t dtype;
+  int32_t param_dtype;
+  int32_t reserved;
+} mfx_norm_bwd_args;
+
+int mfx_layer_norm_bwd(const mfx_norm_bwd_args* args, void* stream);
+
+/* Bytes of workspace mfx_layer_norm_bwd needs for these arguments. */
+size_t mfx_layer_norm_bwd_workspace_size(const mfx_norm_bwd_args* args);
+
+/*
  * Scaled dot-product attention, out = softmax(scale * Q K^T + M) V.
  *
  * Logical shapes q [B, Hq, Tq, D], k [B, Hkv, Tk, D], v [B, Hkv, Tk, Dv],
@@ -152,6 +192,57 @@ size_t mfx_sdpa_workspace_size(const mfx_sdpa_args* args);
 /* Which kernel mfx_sdpa_fwd would launch for these arguments, as a static
  * string ("flash_bf16_d128", "decode_splitkv", ...), or NULL if invalid. */
 const char* mfx_sdpa_kernel_name(const mfx_sdpa_args* args);
+
+/*
+ * SDPA backward: given dO = dL/d(out) of out = softmax(scale * Q K^T + M) V,
+ *   P = softmax(scale * Q K^T + M),  dP = dO V^T,
+ *   dS = P * (dP - rowsum(dO * out)),
+ *   dV = P^T dO,  dQ = scale * dS K,  dK = scale * dS^T Q,
+ * with dK / dV of a kv head summed over its Hq / Hkv query heads (GQA).
+ * Shapes, strides (feature stride 1), causal and mask follow mfx_sdpa_args;
+ * dq / dk / dv have q / k / v's logical shapes and their own strides, and
+ * every tensor has `dtype` (fp32 accumulation).  The forward pass is
+ * recomputed into the workspace (out and the row log-sum-exp), so only the
+ * inputs are needed.  Workspace: mfx_sdpa_bwd_workspace_size() bytes, or
+ * NULL for library scratch.  Deterministic: no atomics.
+ * Replaces mx::vjp of fast::scaled_dot_product_attention behind custom_call
+ * @mlx_sdpa_bwd (reference src/jax_mlx_pjrt.cpp:8151-8206; closed form
+ * src/jax_mlx/sdpa.py:65-87).
+ */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* dout;
+  const void* mask;
+  void* dq;
+  void* dk;
+  void* dv;
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t B, Hq, Hkv, Tq, Tk, D, Dv;
+  int64_t q_strides[4];
+  int64_t k_strides[4];
+  int64_t v_strides[4];
+  int64_t do_strides[4];
+  int64_t dq_strides[4];
+  int64_t dk_strides[4];
+  int64_t dv_strides[4];
+  int64_t mask_strides[4];
+  float scale;
+  int32_t causal;
+  int32_t dtype;
+  int32_t mask_dtype;
+} mfx_sdpa_bwd_args;
+
+int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream);
+
+/* Bytes of workspace mfx_sdpa_bwd needs for these arguments. */
+size_t mfx_sdpa_bwd_workspace_size(const mfx_sdpa_bwd_args* args);
+
+/* Which backward kernels mfx_sdpa_bwd would launch ("mfma_bf16_d128",
+ * "generic", ...), or NULL if the arguments are invalid. */
+const char* mfx_sdpa_bwd_kernel_name(const mfx_sdpa_bwd_args* args);
 
 /* ==========================================================================
  * Generic ops: the graph regions the pattern matcher does not fuse.

@@ -1,0 +1,108 @@
+// Row-vector helpers shared by the forward and backward row kernels: 16-byte
+// vectors of f32 / bf16 unpacked to fp32, parameter loads of either storage
+// type, and sums / maxima over the lanes that own a row.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace mfx {
+namespace rowvec {
+
+constexpr int kBlock = 256;
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  typedef float4 type;
+};
+template <>
+struct Vec16<bf16> {
+  static constexpr int N = 8;
+  typedef uint4 type;
+};
+
+template <typename T>
+__device__ __forceinline__ void unpack16(const typename Vec16<T>::type& v, float* out);
+template <>
+__device__ __forceinline__ void unpack16<float>(const float4& v, float* out) {
+  out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void unpack16<bf16>(const uint4& v, float* out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ typename Vec16<T>::type pack16(const float* in);
+template <>
+__device__ __forceinline__ float4 pack16<float>(const float* in) {
+  return make_float4(in[0], in[1], in[2], in[3]);
+}
+template <>
+__device__ __forceinline__ uint4 pack16<bf16>(const float* in) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16 lo = static_cast<bf16>(in[2 * i]);
+    bf16 hi = static_cast<bf16>(in[2 * i + 1]);
+    w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ float load_param(const void* p, int dt, int i) {
+  if (dt == MFX_F32) return static_cast<const float*>(p)[i];
+  return static_cast<float>(static_cast<const bf16*>(p)[i]);
+}
+
+// VEC consecutive parameters of storage type PT starting at element e, as
+// fp32, in 16-byte (f32) or 8/16-byte (bf16) vector loads.
+template <typename PT, int VEC>
+__device__ __forceinline__ void load_params(const void* p, int e, float* out) {
+  if constexpr (std::is_same<PT, float>::value) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + e);
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) {
+      const float4 v = q[j];
+      out[4 * j] = v.x; out[4 * j + 1] = v.y; out[4 * j + 2] = v.z; out[4 * j + 3] = v.w;
+    }
+  } else if constexpr (VEC == 8) {
+    unpack16<bf16>(*reinterpret_cast<const uint4*>(static_cast<const bf16*>(p) + e), out);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const bf16*>(p) + e);
+    out[0] = __uint_as_float(v.x << 16); out[1] = __uint_as_float(v.x & 0xffff0000u);
+    out[2] = __uint_as_float(v.y << 16); out[3] = __uint_as_float(v.y & 0xffff0000u);
+  }
+}
+
+// Sum / max over the LANES threads that own a row.  For LANES > 64 the
+// partials of the wavefronts meet in LDS.
+template <int LANES, bool kMax>
+__device__ __forceinline__ float row_reduce(float v, float* lds) {
+  if constexpr (LANES <= 64) {
+    return kMax ? group_max<LANES>(v) : group_sum<LANES>(v);
+  } else {
+    v = kMax ? group_max<64>(v) : group_sum<64>(v);
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[wid] = v;
+    __syncthreads();
+    float r = lds[0];
+#pragma unroll
+    for (int i = 1; i < LANES / 64; ++i) r = kMax ? fmaxf(r, lds[i]) : r + lds[i];
+    __syncthreads();
+    return r;
+  }
+}
+
+}  // namespace rowvec
+}  // namespace mfx

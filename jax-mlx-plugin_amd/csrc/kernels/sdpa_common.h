@@ -24,7 +24,39 @@ struct SdpaParams {
   float q_rms_eps;   // < 0: no RMSNorm on q
   int num_splits;    // split-KV decode only: partials per row
   int split_len;     // keys per split (VALU decode; the MFMA decode interleaves tiles)
+  // Optional: row log-sum-exp of the scaled scores in log2 units,
+  // lse[(b * Hq + h) * Tq + i] = log2(sum_j exp2(s_ij)), written by the
+  // flash and generic kernels when non-null (the backward pass reads it).
+  float* lse;
 };
+
+// Backward pass (mfx_sdpa_bwd).  o / lse come from the recomputed forward
+// pass: o contiguous [B][Hq][Tq][Dv] of `dtype`, lse and delta
+// [B][Hq][Tq] fp32 (log2 units for lse; delta = rowsum(dO * o)).
+struct SdpaBwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const void* mask;
+  void* dq;
+  void* dk;
+  void* dv;
+  const float* lse;
+  const float* delta;
+  int64_t qs[4], ks[4], vs[4], dos[4], dqs[4], dks[4], dvs[4], ms[4];
+  int B, Hq, Hkv, Tq, Tk, D, Dv;
+  int group;
+  int mask_dtype;
+  int dtype;
+  int causal;
+  float scale;
+  float scale_log2;
+};
+
+bool bwd_mfma_supports(const SdpaBwdParams& p);
+int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s);  // dQ, dK, dV
 
 // Kernel families; each returns MFX_OK or an error code after launching.
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s);

@@ -178,6 +178,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_f32_kernel(SdpaParams p) {
 
   const float lt = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / lt;
+  if (p.lse && half == 0 && qi < Tq) p.lse[(int64_t)bh * Tq + qi] = m_run + __log2f(lt);
   if (qi < Tq) {
     float* orow = op + qi * os2;
 #pragma unroll

@@ -83,6 +83,7 @@ __global__ __launch_bounds__(64) void generic_kernel(SdpaParams p) {
     }
     __syncthreads();
   }
+  if (p.lse && lane == 0) p.lse[row] = m + __log2f(l);
   T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + t * p.os[2];
 #pragma unroll
   for (int jj = 0; jj < kMaxD / 64; ++jj) {

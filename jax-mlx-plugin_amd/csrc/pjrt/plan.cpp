@@ -227,7 +227,7 @@ class Planner {
   static void check_supported(const Node& n) {
     static const std::set<std::string> ok = {
         "stablehlo.dot_general", "stablehlo.dot", "stablehlo.reduce", "mfx.sdpa", "mfx.layer_norm",
-        "mfx.rms_norm", "mfx.softmax", "stablehlo.concatenate"};
+        "mfx.rms_norm", "mfx.softmax", "mfx.layer_norm_bwd", "stablehlo.concatenate"};
     if (!ok.count(n.op)) {
       std::string what = n.op;
       if (n.op == "stablehlo.custom_call") what += " @" + n.strs.at("target");
@@ -905,6 +905,68 @@ class Planner {
     io_.push_back(io);
   }
 
+  // custom_call @mlx_layer_norm_bwd: (x, gamma, dy) -> (dx, dgamma, dbeta).
+  void emit_norm_bwd(const Node& n) {
+    const int x = n.in[0], gamma = n.in[1], dy = n.in[2];
+    const int dx = n.out[0], dg = n.out[1], db = n.out[2];
+    const Type& t = ty(x);
+    mfx_norm_bwd_args a{};
+    a.n = t.dims.back();
+    a.rows = a.n ? t.numel() / a.n : 0;
+    a.x_row_stride = a.dy_row_stride = a.dx_row_stride = a.n;
+    a.eps = (float)n.nums.at("eps");
+    a.dtype = mfx_dtype(t.dtype);
+    a.param_dtype = mfx_dtype(ty(dg).dtype);
+    if (ty(dy).dtype != t.dtype || ty(dx).dtype != t.dtype || ty(gamma).dtype != ty(dg).dtype)
+      throw ParseError("mlx_layer_norm_bwd: x / grad_out / dx and weight / dweight dtypes must match");
+    if (a.dtype != MFX_F32 && a.dtype != MFX_BF16) throw ParseError("mlx_layer_norm_bwd: x must be f32 or bf16");
+    if (a.param_dtype != MFX_F32 && a.param_dtype != MFX_BF16)
+      throw ParseError("mlx_layer_norm_bwd: weight must be f32 or bf16");
+    check_dense("norm bwd x", x, a.rows * a.n);
+    check_dense("norm bwd dy", dy, a.rows * a.n);
+    check_dense("norm bwd dx", dx, a.rows * a.n);
+    check_dense("norm bwd gamma", gamma, a.n);
+    check_dense("norm bwd dgamma", dg, a.n);
+    check_dense("norm bwd dbeta", db, a.n);
+    mfx_norm_bwd_args probe = a;
+    probe.x = probe.dy = probe.gamma = (void*)0x10000;
+    probe.dx = probe.dgamma = probe.dbeta = (void*)0x10000;
+    const size_t ws = mfx_layer_norm_bwd_workspace_size(&probe);
+    int ws_v = -1;
+    if (ws > 0) {
+      Type wt;
+      wt.dtype = DType::kU8;
+      wt.dims = {(int64_t)ws};
+      ws_v = new_temp(wt);
+    }
+    auto loc = loc_;
+    Plan* plan = &plan_;
+    Step s;
+    s.kind = "layer_norm_bwd";
+    s.label = "mfx.layer_norm_bwd";
+    s.bytes = 3.0 * t.bytes();
+    s.run = [a, x, gamma, dy, dx, dg, db, ws_v, ws, loc, plan](const ExecBuffers& b, std::string& err) {
+      mfx_norm_bwd_args r = a;
+      r.x = plan->ptr((*loc)[x], b);
+      r.gamma = plan->ptr((*loc)[gamma], b);
+      r.dy = plan->ptr((*loc)[dy], b);
+      r.dx = plan->ptr((*loc)[dx], b);
+      r.dgamma = plan->ptr((*loc)[dg], b);
+      r.dbeta = plan->ptr((*loc)[db], b);
+      if (ws_v >= 0) {
+        r.workspace = plan->ptr((*loc)[ws_v], b);
+        r.workspace_bytes = ws;
+      }
+      int rc = mfx_layer_norm_bwd(&r, b.stream);
+      if (rc != MFX_OK) err = mfx_last_error();
+      return rc;
+    };
+    plan_.steps_.push_back(std::move(s));
+    StepIO io{{x, gamma, dy}, {dx, dg, db}};
+    if (ws_v >= 0) io.writes.push_back(ws_v);
+    io_.push_back(io);
+  }
+
   void emit_sdpa(const Node& n) {
     const auto& sh = n.ints.at("shape");
     mfx_sdpa_args a{};
@@ -1101,6 +1163,7 @@ class Planner {
         else if (n.op == "stablehlo.reduce") emit_reduce(n);
         else if (n.op == "mfx.sdpa") emit_sdpa(n);
         else if (n.op == "stablehlo.concatenate") emit_concat(n);
+        else if (n.op == "mfx.layer_norm_bwd") emit_norm_bwd(n);
         else emit_norm(n);
         continue;
       }

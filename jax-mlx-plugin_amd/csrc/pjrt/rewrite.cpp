@@ -1191,6 +1191,30 @@ int rewrite_custom_calls(Ctx& c, RewriteStats& st) {
       st.custom_calls++;
       st.layer_norm++;
       ++count;
+    } else if (target == "mlx_layer_norm_bwd") {
+      // (x, weight, bias, grad_out) -> (dx, dweight, dbias); bias only fixes
+      // the dbias type (reference src/jax_mlx/layer_norm.py:46-56).
+      if (n.in.size() != 4 || n.out.size() != 3)
+        throw ParseError("mlx_layer_norm_bwd expects 4 operands and 3 results");
+      const Type& xt = c.ty(n.in[0]);
+      const Type& wt = c.ty(n.in[1]);
+      if (xt.rank() < 1 || wt.rank() != 1 || wt.dims[0] != xt.dims.back())
+        throw ParseError("mlx_layer_norm_bwd weight must be [N] for x [..., N]");
+      if (c.ty(n.in[3]).dims != xt.dims || c.ty(n.out[0]).dims != xt.dims)
+        throw ParseError("mlx_layer_norm_bwd grad_out and dx must have x's shape");
+      if (c.ty(n.out[1]).dims != wt.dims || c.ty(n.out[2]).dims != wt.dims ||
+          c.ty(n.out[1]).dtype != c.ty(n.out[2]).dtype)
+        throw ParseError("mlx_layer_norm_bwd dweight and dbias must be [N] of one dtype");
+      double eps = 1e-5;
+      json_number(cfg, "eps", eps);
+      Node f;
+      f.op = "mfx.layer_norm_bwd";
+      f.in = {n.in[0], n.in[1], n.in[3]};
+      f.out = n.out;
+      f.nums["eps"] = eps;
+      n = f;
+      st.custom_calls++;
+      ++count;
     }
   }
   if (count) c.refresh();

@@ -41,6 +41,28 @@ class NormArgs(ctypes.Structure):
     ]
 
 
+class NormBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("gamma", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("dx", ctypes.c_void_p),
+        ("dgamma", ctypes.c_void_p),
+        ("dbeta", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("x_row_stride", ctypes.c_int64),
+        ("dy_row_stride", ctypes.c_int64),
+        ("dx_row_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 I64x4 = ctypes.c_int64 * 4
 
 
@@ -75,6 +97,40 @@ class SdpaArgs(ctypes.Structure):
     ]
 
 
+class SdpaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("B", ctypes.c_int64),
+        ("Hq", ctypes.c_int64),
+        ("Hkv", ctypes.c_int64),
+        ("Tq", ctypes.c_int64),
+        ("Tk", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("Dv", ctypes.c_int64),
+        ("q_strides", I64x4),
+        ("k_strides", I64x4),
+        ("v_strides", I64x4),
+        ("do_strides", I64x4),
+        ("dq_strides", I64x4),
+        ("dk_strides", I64x4),
+        ("dv_strides", I64x4),
+        ("mask_strides", I64x4),
+        ("scale", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("mask_dtype", ctypes.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -95,6 +151,16 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.POINTER(NormArgs), ctypes.c_void_p]
         fn.restype = ctypes.c_int
+    lib.mfx_layer_norm_bwd.argtypes = [ctypes.POINTER(NormBwdArgs), ctypes.c_void_p]
+    lib.mfx_layer_norm_bwd.restype = ctypes.c_int
+    lib.mfx_layer_norm_bwd_workspace_size.argtypes = [ctypes.POINTER(NormBwdArgs)]
+    lib.mfx_layer_norm_bwd_workspace_size.restype = ctypes.c_size_t
+    lib.mfx_sdpa_bwd.argtypes = [ctypes.POINTER(SdpaBwdArgs), ctypes.c_void_p]
+    lib.mfx_sdpa_bwd.restype = ctypes.c_int
+    lib.mfx_sdpa_bwd_workspace_size.argtypes = [ctypes.POINTER(SdpaBwdArgs)]
+    lib.mfx_sdpa_bwd_workspace_size.restype = ctypes.c_size_t
+    lib.mfx_sdpa_bwd_kernel_name.argtypes = [ctypes.POINTER(SdpaBwdArgs)]
+    lib.mfx_sdpa_bwd_kernel_name.restype = ctypes.c_char_p
     lib.mfx_sdpa_fwd.argtypes = [ctypes.POINTER(SdpaArgs), ctypes.c_void_p]
     lib.mfx_sdpa_fwd.restype = ctypes.c_int
     lib.mfx_sdpa_workspace_size.argtypes = [ctypes.POINTER(SdpaArgs)]
@@ -195,6 +261,47 @@ def softmax(x, out=None):
     return _norm_call("mfx_softmax", x, None, None, 0.0, out)
 
 
+def layer_norm_bwd(x, dy, gamma=None, eps: float = 1e-5, *, param_grads=True, param_dtype=None,
+                   dx=None, workspace=None):
+    """(dx, dgamma, dbeta) of LayerNorm over the last axis (mfx_layer_norm_bwd).
+
+    dgamma / dbeta have gamma's dtype (or `param_dtype`, default x's dtype when
+    gamma is None); with param_grads=False only dx is computed."""
+    torch = _torch()
+    _require_gpu(x, dy, gamma)
+    if dx is None:
+        dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    rows, n, xs = _rows_view(x)
+    _, _, gs = _rows_view(dy)
+    _, _, ds = _rows_view(dx)
+    pdt = gamma.dtype if gamma is not None else (param_dtype or x.dtype)
+    dg = db = None
+    if param_grads:
+        dg = torch.empty(n, dtype=pdt, device=x.device)
+        db = torch.empty(n, dtype=pdt, device=x.device)
+    a = NormBwdArgs(
+        x=x.data_ptr(), gamma=gamma.data_ptr() if gamma is not None else None, dy=dy.data_ptr(),
+        dx=dx.data_ptr(), dgamma=dg.data_ptr() if dg is not None else None,
+        dbeta=db.data_ptr() if db is not None else None, rows=rows, n=n, x_row_stride=xs,
+        dy_row_stride=gs, dx_row_stride=ds, eps=float(eps), dtype=dtype_code(x.dtype),
+        param_dtype=dtype_code(pdt))
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    check(load().mfx_layer_norm_bwd(ctypes.byref(a), ctypes.c_void_p(_stream_handle(x))))
+    return dx, dg, db
+
+
+def layer_norm_bwd_workspace_size(x, gamma=None, param_grads=True) -> int:
+    """Bytes of workspace mfx_layer_norm_bwd needs (host-only query)."""
+    rows, n, xs = _rows_view(x)
+    a = NormBwdArgs(x=16, dy=16, dx=16, dgamma=16 if param_grads else None,
+                    dbeta=16 if param_grads else None, rows=rows, n=n, x_row_stride=xs,
+                    dy_row_stride=n, dx_row_stride=n, eps=1e-5, dtype=dtype_code(x.dtype),
+                    param_dtype=dtype_code(gamma.dtype if gamma is not None else x.dtype))
+    return int(load().mfx_layer_norm_bwd_workspace_size(ctypes.byref(a)))
+
+
 def _strides4(t, layout: str):
     s = t.stride()
     if layout == "bhtd":
@@ -272,3 +379,60 @@ def sdpa_kernel_name(q, k, v, **kw) -> str:
     if name is None:
         raise MfxError(-1, load().mfx_last_error().decode())
     return name.decode()
+
+
+def sdpa_bwd_args(q, k, v, dout, dq, dk, dv, *, scale=None, causal=False, mask=None, layout="bhtd",
+                  workspace=None) -> SdpaBwdArgs:
+    B, Hq, Tq, D = _dims(q, layout)
+    _, Hkv, Tk, _ = _dims(k, layout)
+    Dv = v.shape[-1]
+    if scale is None:
+        scale = 1.0 / (D ** 0.5)
+    a = SdpaBwdArgs()
+    a.q, a.k, a.v, a.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr()
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    a.B, a.Hq, a.Hkv, a.Tq, a.Tk, a.D, a.Dv = B, Hq, Hkv, Tq, Tk, D, Dv
+    for name, t in (("q_strides", q), ("k_strides", k), ("v_strides", v), ("do_strides", dout),
+                    ("dq_strides", dq), ("dk_strides", dk), ("dv_strides", dv)):
+        setattr(a, name, I64x4(*_strides4(t, layout)))
+    a.scale = float(scale)
+    a.causal = 1 if causal else 0
+    a.dtype = dtype_code(q.dtype)
+    if mask is not None:
+        m = mask
+        while m.dim() < 4:
+            m = m.unsqueeze(0)
+        ms = [0 if m.shape[i] == 1 else m.stride(i) for i in range(4)]
+        a.mask = m.data_ptr()
+        a.mask_strides = I64x4(*ms)
+        a.mask_dtype = dtype_code(m.dtype)
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    return a
+
+
+def sdpa_bwd(q, k, v, dout, *, scale=None, causal=False, mask=None, layout="bhtd", workspace=None):
+    """(dq, dk, dv) of softmax(scale * Q K^T + mask) V for upstream gradient dout
+    (mfx_sdpa_bwd); layouts as sdpa()."""
+    torch = _torch()
+    _require_gpu(q, k, v, dout, mask)
+    dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
+    a = sdpa_bwd_args(q, k, v, dout, dq, dk, dv, scale=scale, causal=causal, mask=mask, layout=layout,
+                      workspace=workspace)
+    check(load().mfx_sdpa_bwd(ctypes.byref(a), ctypes.c_void_p(_stream_handle(q))))
+    return dq, dk, dv
+
+
+def sdpa_bwd_kernel_name(q, k, v, **kw) -> str:
+    """Which backward kernels mfx_sdpa_bwd picks (host-only query)."""
+    a = sdpa_bwd_args(q, k, v, q, q, k, v, **kw)
+    name = load().mfx_sdpa_bwd_kernel_name(ctypes.byref(a))
+    if name is None:
+        raise MfxError(-1, load().mfx_last_error().decode())
+    return name.decode()
+
+
+def sdpa_bwd_workspace_size(q, k, v, **kw) -> int:
+    a = sdpa_bwd_args(q, k, v, q, q, k, v, **kw)
+    return int(load().mfx_sdpa_bwd_workspace_size(ctypes.byref(a)))

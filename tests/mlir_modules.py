@@ -397,6 +397,22 @@ def custom_call_layer_norm_module(shape=(4, 512), eps=1e-5, dt="f32"):
     return module("jit_mlx_layer_norm", [f.text([o], [ty(shape, dt)])])
 
 
+def custom_call_layer_norm_bwd_module(shape=(4, 512), eps=1e-5, dt="f32", pdt=None):
+    """custom_call @mlx_layer_norm_bwd (src/jax_mlx/layer_norm.py:102-116):
+    (x, weight, bias, grad_out) -> (dx, dweight, dbias)."""
+    shape = list(shape)
+    pdt = pdt or dt
+    C = shape[-1]
+    f = Fn("main", [(shape, dt), ([C], pdt), ([C], pdt), (shape, dt)])
+    cfg = '{\\22eps\\22: ' + repr(float(eps)) + '}'
+    rts = [ty(shape, dt), ty([C], pdt), ty([C], pdt)]
+    r = f.new()
+    f.lines.append(f'    {r}:3 = stablehlo.custom_call @mlx_layer_norm_bwd(%arg0, %arg1, %arg2, %arg3) '
+                   f'{{backend_config = "{cfg}"}} : ({ty(shape, dt)}, {ty([C], pdt)}, {ty([C], pdt)}, '
+                   f'{ty(shape, dt)}) -> ({", ".join(rts)})')
+    return module("jit_mlx_layer_norm_bwd", [f.text([f"{r}#0", f"{r}#1", f"{r}#2"], rts)])
+
+
 # ---------------------------------------------------------------- transformer
 
 def transformer_module(layers=4, B=32, T=256, d=512, heads=8, mlp=2048, eps=1e-5, dt="f32", causal=False):

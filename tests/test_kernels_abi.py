@@ -106,6 +106,32 @@ def test_invalid_arguments_are_rejected_on_host(native):
     # Zero rows is a valid no-op that touches no memory.
     na.x, na.rows = 1, 0
     assert lib.mfx_layer_norm(ctypes.byref(na), None) == 0
+    # LayerNorm backward: short strides, null dx, bad dtypes are host errors.
+    ba = native.NormBwdArgs(x=16, dy=16, dx=16, rows=4, n=8, x_row_stride=8, dy_row_stride=4,
+                            dx_row_stride=8, eps=1e-5, dtype=native.MFX_F32, param_dtype=native.MFX_F32)
+    assert lib.mfx_layer_norm_bwd(ctypes.byref(ba), None) == -1
+    ba.dy_row_stride, ba.dx = 8, None
+    assert lib.mfx_layer_norm_bwd(ctypes.byref(ba), None) == -1
+    ba.dx, ba.dtype = 16, native.MFX_F16
+    assert lib.mfx_layer_norm_bwd(ctypes.byref(ba), None) == -1 and b"dtype" in lib.mfx_last_error()
+
+
+def test_layer_norm_bwd_workspace_is_sized(native):
+    import torch
+
+    lib = native.load()
+    x = torch.zeros(8 * 128, 512)
+    # 1024 rows of 128 vectors: 64 lanes a row, 4 rows a workgroup, 2 rows a
+    # group -> 128 partial row pairs of 512 floats.
+    assert native.layer_norm_bwd_workspace_size(x) == 128 * 2 * 512 * 4
+    assert native.layer_norm_bwd_workspace_size(x, param_grads=False) == 0
+    # Partial rows are capped at 1024 however many rows there are.
+    big = torch.empty(1 << 20, 64)
+    assert native.layer_norm_bwd_workspace_size(big) == 1024 * 2 * 64 * 4
+    ba = native.NormBwdArgs(x=16, dy=16, dx=16, dgamma=16, rows=0, n=8, x_row_stride=8,
+                            dy_row_stride=8, dx_row_stride=8, eps=1e-5, dtype=native.MFX_F32,
+                            param_dtype=native.MFX_F32)
+    assert lib.mfx_layer_norm_bwd_workspace_size(ctypes.byref(ba)) == 0
 
 
 def test_calls_fail_loudly_without_a_gpu(native):

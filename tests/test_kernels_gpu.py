@@ -82,6 +82,73 @@ def test_layer_norm_strided_rows_and_constant_rows(cuda, nat, oracle):
     assert cuda.equal(yc, beta.expand(4, 512))
 
 
+
+# ------------------------------------------------------- LayerNorm backward
+# mfx_layer_norm_bwd against the fp64 oracle (reference closed form
+# src/jax_mlx/layer_norm.py:59-76).  f32: ||out - ref||_inf <= 1e-5 *
+# max(1, ||ref||_inf) for dx, dgamma and dbeta (the parameter sums add up to
+# 65536 rows); bf16 inputs: the bf16 relative bar.
+
+def _ln_bwd_case(cuda, nat, oracle, shape, dtype, pdtype, seed, gamma=True):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(shape).astype(np.float32) * 2 + 0.5
+    dy = rng.standard_normal(shape).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    xd, dyd = dev(cuda, x, dtype), dev(cuda, dy, dtype)
+    gd = dev(cuda, g, pdtype) if gamma else None
+    dx, dg, db = nat.layer_norm_bwd(xd, dyd, gd, eps=1e-5, param_dtype=pdtype)
+    n = shape[-1]
+    ref = oracle.layer_norm_bwd(host(xd).reshape(-1, n), host(gd) if gamma else None,
+                                host(dyd).reshape(-1, n), 1e-5)
+    return [host(t).reshape(r.shape) for t, r in zip((dx, dg, db), ref)], ref
+
+
+def _check_f32(outs, refs, tol=F32_NORM_TOL):
+    for o, r in zip(outs, refs):
+        assert np.abs(o - r).max() <= tol * max(1.0, np.abs(r).max()), np.abs(o - r).max()
+
+
+@pytest.mark.parametrize("shape", [(8, 128, 512), (3, 8), (5, 100), (1025, 512), (7, 1000),
+                                   (4, 4096), (3, 6000), (2, 64), (33, 77), (65536, 64)])
+def test_layer_norm_bwd_f32(cuda, nat, oracle, shape):
+    outs, refs = _ln_bwd_case(cuda, nat, oracle, shape, cuda.float32, cuda.float32, 11)
+    _check_f32(outs, refs)
+
+
+@pytest.mark.parametrize("shape", [(8, 128, 512), (33, 128), (4, 4096), (3, 40), (5, 8200), (9, 30)])
+@pytest.mark.parametrize("pbf16", [False, True])
+def test_layer_norm_bwd_bf16(cuda, nat, oracle, shape, pbf16):
+    outs, refs = _ln_bwd_case(cuda, nat, oracle, shape, cuda.bfloat16,
+                              cuda.bfloat16 if pbf16 else cuda.float32, 12)
+    for o, r in zip(outs, refs):
+        assert rel_inf(o, r) <= BF16_REL_TOL
+
+
+def test_layer_norm_bwd_without_gamma_strided_and_empty(cuda, nat, oracle):
+    outs, refs = _ln_bwd_case(cuda, nat, oracle, (64, 256), cuda.float32, cuda.float32, 13, gamma=False)
+    _check_f32(outs, refs)
+    rng = np.random.default_rng(14)
+    big = dev(cuda, rng.standard_normal((48, 1024)), cuda.float32)
+    gbig = dev(cuda, rng.standard_normal((48, 768)), cuda.float32)
+    x, dy = big[:, 256:768], gbig[:, 128:640]  # row strides 1024 and 768
+    gam = dev(cuda, 1 + 0.1 * rng.standard_normal(512), cuda.float32)
+    dx, dg, db = nat.layer_norm_bwd(x, dy, gam, eps=1e-5)
+    ref = oracle.layer_norm_bwd(host(x), host(gam), host(dy), 1e-5)
+    _check_f32([host(dx), host(dg), host(db)], ref)
+    # dx only: the parameter sums are skipped, dx is unchanged.
+    dx2, dg2, db2 = nat.layer_norm_bwd(x, dy, gam, eps=1e-5, param_grads=False)
+    assert dg2 is None and db2 is None
+    assert np.array_equal(host(dx2), host(dx))
+    # No rows: dx is empty and the parameter gradients are zero sums.
+    e = cuda.empty((0, 512), device="cuda")
+    dx3, dg3, db3 = nat.layer_norm_bwd(e, e, gam, eps=1e-5)
+    assert dx3.numel() == 0 and np.all(host(dg3) == 0) and np.all(host(db3) == 0)
+    # Caller workspace of the queried size gives identical results.
+    ws = cuda.empty(nat.layer_norm_bwd_workspace_size(x, gam), dtype=cuda.uint8, device="cuda")
+    dx4, dg4, db4 = nat.layer_norm_bwd(x, dy, gam, eps=1e-5, workspace=ws)
+    assert np.array_equal(host(dg4), host(dg)) and np.array_equal(host(db4), host(db))
+
+
 @pytest.mark.parametrize("dtype,shape", [("f32", (2, 4, 128)), ("f32", (9, 4096)), ("f32", (3, 77)),
                                          ("bf16", (16, 32, 1, 128)), ("bf16", (5, 2048))])
 def test_rms_norm(cuda, nat, oracle, dtype, shape):
@@ -305,3 +372,90 @@ def test_sdpa_decode_mfma_fully_masked_row_is_nan(cuda, nat):
     out = nat.sdpa(q, k, v, scale=0.125, mask=mask).float()
     assert bool(cuda.isnan(out[:, 1]).all())
     assert bool(cuda.isfinite(out[:, [0, 2, 3]]).all())
+
+
+# ---------------------------------------------------------- SDPA backward
+# mfx_sdpa_bwd against the fp64 oracle (reference closed form
+# src/jax_mlx/sdpa.py:65-87; masks and GQA as the forward).  f32:
+# ||d - ref||_inf <= 1e-4 * max(1, ||ref||_inf) per gradient; bf16: the
+# relative bar on each of dq, dk, dv.
+
+def check_grads(outs, refs, dtype):
+    for name, o, r in zip(("dq", "dk", "dv"), outs, refs):
+        o = host(o)
+        if dtype == "f32":
+            err = np.abs(o - r).max()
+            assert err <= F32_SDPA_TOL * max(1.0, np.abs(r).max()), (name, err)
+        else:
+            rr = rel_inf(o, r)
+            assert rr <= BF16_REL_TOL, (name, rr)
+
+
+def bwd_case(cuda, nat, oracle, seed, qshape, kshape, dtype, *, causal=False, scale=None, mask=None,
+             vshape=None, layout="bhtd"):
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    q, k, v = make_qkv(cuda, seed, qshape, kshape, td, vshape)
+    rng = np.random.default_rng(seed + 100)
+    oshape = list(qshape)
+    oshape[-1] = (vshape or kshape)[-1]
+    g = dev(cuda, rng.standard_normal(oshape), td)
+    grads = nat.sdpa_bwd(q, k, v, g, scale=scale, causal=causal, mask=mask, layout=layout)
+    tr = (lambda a: a.transpose(0, 2, 1, 3)) if layout == "bthd" else (lambda a: a)
+    D = qshape[-1]
+    sc = scale if scale is not None else 1.0 / np.sqrt(D)
+    refs = oracle.sdpa_bwd(tr(host(q)), tr(host(k)), tr(host(v)), tr(host(g)), sc, causal=causal,
+                           mask=None if mask is None else host(mask))
+    return grads, [tr(r) for r in refs]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_bwd_f32_config2(cuda, nat, oracle, causal):
+    grads, refs = bwd_case(cuda, nat, oracle, 2, (8, 8, 128, 64), (8, 8, 128, 64), "f32", causal=causal,
+                           scale=0.125)
+    check_grads(grads, refs, "f32")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("D,tq,tk,causal", [(128, 64, 64, True), (64, 256, 256, False), (128, 200, 200, True),
+                                            (64, 77, 130, False), (128, 1, 33, False), (64, 130, 130, True)])
+def test_sdpa_bwd_shapes(cuda, nat, oracle, dtype, D, tq, tk, causal):
+    grads, refs = bwd_case(cuda, nat, oracle, 31, (1, 2, tq, D), (1, 2, tk, D), dtype, causal=causal)
+    check_grads(grads, refs, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sdpa_bwd_btnh_gqa_mask(cuda, nat, oracle, dtype):
+    """BTNH layout (the custom_call @mlx_sdpa_bwd operands), Hq 8 over Hkv 2,
+    additive mask broadcast over heads, -inf holes."""
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    rng = np.random.default_rng(41)
+    m = rng.standard_normal((2, 1, 96, 160)).astype(np.float32)
+    m[:, :, :, 5] = -np.inf
+    mask = dev(cuda, m, td)
+    grads, refs = bwd_case(cuda, nat, oracle, 42, (2, 96, 8, 64), (2, 160, 2, 64), dtype, mask=mask,
+                           layout="bthd", scale=0.2)
+    check_grads(grads, refs, dtype)
+
+
+def test_sdpa_bwd_odd_head_size_generic(cuda, nat, oracle):
+    grads, refs = bwd_case(cuda, nat, oracle, 43, (1, 3, 50, 80), (1, 3, 70, 80), "bf16", causal=True,
+                           vshape=(1, 3, 70, 48))
+    check_grads(grads, refs, "bf16")
+
+
+def test_sdpa_bwd_known_answers(cuda, nat):
+    """Tk = 1: out = v, so dv = sum over query rows of dO and dq = dk = 0.
+    Identical keys: P is uniform 1/Tk, so dq = 0 and every dv_j is the sum of
+    dO over query rows divided by Tk."""
+    q = cuda.randn(1, 1, 8, 64, device="cuda")
+    k = cuda.randn(1, 1, 1, 64, device="cuda")
+    v = cuda.randn(1, 1, 1, 64, device="cuda")
+    g = cuda.randn(1, 1, 8, 64, device="cuda")
+    dq, dk, dv = nat.sdpa_bwd(q, k, v, g)
+    assert np.abs(host(dq)).max() <= 1e-5 and np.abs(host(dk)).max() <= 1e-5
+    np.testing.assert_allclose(host(dv)[0, 0, 0], host(g).sum(axis=2)[0, 0], atol=1e-5)
+    k = cuda.randn(1, 1, 1, 64, device="cuda").expand(1, 1, 16, 64).contiguous()
+    v = cuda.randn(1, 1, 16, 64, device="cuda")
+    dq, dk, dv = nat.sdpa_bwd(q, k, v, g)
+    assert np.abs(host(dq)).max() <= 1e-5
+    np.testing.assert_allclose(host(dv)[0, 0], np.tile(host(g).sum(axis=2)[0, 0] / 16, (16, 1)), atol=1e-5)

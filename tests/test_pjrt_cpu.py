@@ -289,6 +289,10 @@ def test_custom_calls(api):
     d = api.inspect(M.custom_call_layer_norm_module(eps=1e-3))
     (n,) = fused(d)
     assert n["op"] == "mfx.layer_norm" and math.isclose(n["f:eps"], 1e-3, rel_tol=1e-6)
+    d = api.inspect(M.custom_call_layer_norm_bwd_module(shape=(8, 128, 512), eps=1e-4))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.layer_norm_bwd" and math.isclose(n["f:eps"], 1e-4, rel_tol=1e-6)
+    assert steps(d) == ["layer_norm_bwd"] and d["plan"]["arena_bytes"] > 0  # parameter partials
 
 
 def test_transformer_plan(api):

@@ -89,6 +89,33 @@ def test_custom_call_layer_norm(client, oracle):
     assert np.abs(y - oracle.layer_norm(x, g, b, 1e-3)).max() <= F32_NORM_TOL
 
 
+@pytest.mark.parametrize("shape,dt,pdt", [((8, 128, 512), "f32", "f32"), ((4, 512), "f32", "f32"),
+                                          ((33, 1000), "f32", "f32"), ((16, 64, 768), "bf16", "f32"),
+                                          ((16, 64, 768), "bf16", "bf16")])
+def test_custom_call_layer_norm_bwd(client, oracle, shape, dt, pdt):
+    """custom_call @mlx_layer_norm_bwd (reference src/jax_mlx_pjrt.cpp:8237-8281)
+    against the fp64 closed form; f32 bar ||d||_inf <= 1e-5 * max(1, ||ref||_inf)."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal(shape).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    b = (0.1 * rng.standard_normal(shape[-1])).astype(np.float32)
+    g = rng.standard_normal(shape).astype(np.float32)
+    if dt == "bf16":
+        x, g = bf16_round(x), bf16_round(g)
+    if pdt == "bf16":
+        w, b = bf16_round(w), bf16_round(b)
+    outs = run(client, M.custom_call_layer_norm_bwd_module(shape, eps=1e-5, dt=dt, pdt=pdt), [x, w, b, g],
+               [dt, pdt, pdt, dt])
+    n = shape[-1]
+    refs = oracle.layer_norm_bwd(x.reshape(-1, n), w, g.reshape(-1, n), 1e-5)
+    for o, r in zip(outs, refs):
+        o = o.reshape(r.shape)
+        if dt == "f32":
+            assert np.abs(o - r).max() <= F32_NORM_TOL * max(1.0, np.abs(r).max())
+        else:
+            assert rel_inf(o, r) <= BF16_REL_TOL
+
+
 @pytest.mark.parametrize("dt,upcast", [("f32", False), ("bf16", True)])
 def test_rms_norm(client, oracle, dt, upcast):
     rng = np.random.default_rng(13)
