@@ -1,12 +1,449 @@
-// Matrix-core SDPA backward (bf16, head size 64 / 128).
-#include "sdpa_common.h"
+// Flash-attention backward on the matrix cores: bf16 inputs, head size 64 or
+// 128 (D == Dv), fp32 accumulation, v_mfma_f32_32x32x16_bf16 throughout.
+//
+// Two kernels, each owning its outputs (deterministic, no atomics):
+//
+// dkdv: workgroup = 4 wavefronts = 128 keys of one (batch, kv head); each
+//   wavefront owns 32 keys.  Its K and V rows stay in registers as the B
+//   operands; Q and dO stream through LDS in 64-query tiles (LDS-DMA, two
+//   stages) over every query head of the kv head's group, with the rows'
+//   lse / delta riding along as two 256-byte DMA rows.  Per 32-query block:
+//     S  = Q K^T     A = Q tile rows        B = K (registers)
+//     dP = dO V^T    A = dO tile rows       B = V (registers)
+//   The 32x32 accumulators give lane l key (l % 32) and 16 query rows, so
+//     P  = exp2(S * s * log2e - lse_q),  dS = P * (dP - delta_q)
+//   are per-element lane work, and both feed the next products as B operands
+//   straight from registers (contraction over queries, permuted identically
+//   in A and B, as in the forward kernel's P V product):
+//     dV^T += dO^T P   A = dO^T from the transposing LDS read
+//     dK^T += Q^T dS   A = Q^T  from the transposing LDS read
+//
+// dq: workgroup = 4 wavefronts = 128 queries of one (batch, head), each
+//   owning 32; Q and dO rows in registers, K and V stream in 64-key tiles as
+//   in the forward kernel:
+//     S^T = K Q^T, dP^T = V dO^T   (lane = query: lse / delta are scalars)
+//     dQ^T += K^T dS^T             A = K^T from the transposing LDS read
+//
+// Tiles use the forward kernel's XOR swizzle, so every operand read is bank
+// conflict free; causal tiles that see nothing are skipped, diagonal and
+// ragged tiles mask per element.
+#include <type_traits>
+
+#include "sdpa_tiles.h"
 
 namespace mfx {
+namespace {
 
-bool bwd_mfma_supports(const SdpaBwdParams& p) { return false; }
+constexpr int kNT = 256;  // 4 wavefronts
+constexpr int kTile = 64;  // streamed rows per tile (queries in dkdv, keys in dq)
+constexpr int kRows = 128;  // owned rows per workgroup (keys in dkdv, queries in dq)
+
+using tiles::lds_s16x4_t;
+using tiles::s16x4;
+using tiles::tile_swz;
+using tiles::wait_dma;
+template <int D>
+using Loader = tiles::TileLoader<D, kTile, kNT / 64>;
+
+// A operand of a 32 x 16 block of the transposed tile: rows d = dt*32 + l32
+// of the tile's [rows x D] storage, k-slots = tile rows ks*16 + {4*half + e,
+// 4*half + 8 + e} (e < 4), the order in which a 32x32 accumulator's 16 rows
+// per lane pair are packed into the two k-steps of a B operand.
+template <int D>
+struct TrReader {
+  int row, sw, sw8, chunk, sub;
+  __device__ __forceinline__ TrReader(int lane) {
+    const int half = lane >> 5, tj = lane & 15, tg = (lane >> 4) & 1;
+    row = 4 * half + (tj >> 2);
+    sw = tile_swz<D>(row);
+    sw8 = tile_swz<D>(row + 8);
+    chunk = tg * 2 + ((tj & 3) >> 1);
+    sub = (tj & 1) * 4;
+  }
+  __device__ __forceinline__ bf16x8 read(const bf16* tile, int ks, int dt) const {
+    const bf16* rows = tile + (ks * 16 + row) * D + sub;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(rows + ((dt * 4 + chunk) ^ sw) * 8));
+    const s16x4 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(rows + 8 * D + ((dt * 4 + chunk) ^ sw8) * 8));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
+// A operand of tile rows mt*32 + l32, feature chunk kk (16 features).
+template <int D>
+__device__ __forceinline__ bf16x8 row_frag(const bf16* tile, int mt, int kk, int l32, int half, int sw) {
+  return *reinterpret_cast<const bf16x8*>(&tile[(mt * 32 + l32) * D + ((kk * 2 + half) ^ sw) * 8]);
+}
+
+// Row `r` (clamped into range, zero past `n`) as D/16 B-operand fragments:
+// fragment kk holds features kk*16 + half*8 .. +7.
+template <int D>
+__device__ __forceinline__ void load_frags(const bf16* base, int64_t stride, int r, int n, int half, bf16x8* f) {
+  const bf16* row = base + (int64_t)min(r, n - 1) * stride + half * 8;
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    u32x4 raw = *reinterpret_cast<const u32x4*>(row + kk * 16);
+    if (r >= n) raw = u32x4{0u, 0u, 0u, 0u};
+    f[kk] = __builtin_bit_cast(bf16x8, raw);
+  }
+}
+
+// Stores a transposed accumulator (rows d, lane column = one output row) as
+// bf16, 4 features per store, times `mul`.
+template <int D>
+__device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int half, float mul) {
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      bf16x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(acc[dt][g * 4 + e] * mul);
+      *reinterpret_cast<bf16x4*>(row + dt * 32 + g * 8 + half * 4) = w;
+    }
+}
+
+// ----------------------------------------------------------------- dK, dV
+
+template <int D, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 q0[kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 g0[kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 q1[kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 g1[kTile * D];
+  __shared__ __attribute__((aligned(16))) float st0[2 * kTile];  // lse | delta
+  __shared__ __attribute__((aligned(16))) float st1[2 * kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int BHk = p.B * p.Hkv;
+  // Key blocks in ascending order: under a causal mask the first key blocks
+  // see the most queries, so the longest blocks are issued first.
+  const int id = blockIdx.x;
+  const int bhk = id % BHk, kblk = id / BHk;
+  const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
+  const int Tq = p.Tq, Tk = p.Tk, G = p.group;
+  const int kw = kblk * kRows + wave * 32;  // this wave's first key
+  const int key = kw + l32;
+
+  const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+  const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+  // Query heads hk*G .. hk*G + G-1 share one resource; tile (g, qt) starts
+  // g * qs[1] + qt * 64 * qs[2] elements past the group's first head.
+  const bf16* qp = static_cast<const bf16*>(p.q) + b * p.qs[0] + (int64_t)hk * G * p.qs[1];
+  const bf16* gp = static_cast<const bf16*>(p.dout) + b * p.dos[0] + (int64_t)hk * G * p.dos[1];
+  const int64_t rbase = ((int64_t)b * p.Hq + (int64_t)hk * G) * Tq;  // lse / delta row of (g=0, q=0)
+  const float* lsep = p.lse + rbase;
+  const float* dlp = p.delta + rbase;
+  const int st_bytes = G * Tq * 4;
+
+  const int qt0 = CAUSAL ? (kblk * kRows) / kTile : 0;
+  const int nqt = (Tq + kTile - 1) / kTile;
+  const int per_head = nqt > qt0 ? nqt - qt0 : 0;
+  const int ntiles = G * per_head;
+
+  // Resource extents end with the last element of the group's last row, so
+  // rows past Tq read zeros or (inside the span) rows of the next head,
+  // which are masked.
+  Loader<D> qload(qp, p.qs[2], 0, wave, lane), gload(gp, p.dos[2], 0, wave, lane);
+  qload.nbytes = (int)(((int64_t)(G - 1) * p.qs[1] + (int64_t)(Tq - 1) * p.qs[2] + D) * 2);
+  gload.nbytes = (int)(((int64_t)(G - 1) * p.dos[1] + (int64_t)(Tq - 1) * p.dos[2] + D) * 2);
+  auto tile_head = [&](int t) { return t / per_head; };
+  auto tile_q = [&](int t) { return qt0 + t % per_head; };
+  auto issue = [&](int t, bf16* ql, bf16* gl, float* sl) {
+    const int g = tile_head(t), qt = tile_q(t);
+    qload.load_at((uint32_t)(((int64_t)g * p.qs[1] + (int64_t)qt * kTile * p.qs[2]) * 2), ql, wave);
+    gload.load_at((uint32_t)(((int64_t)g * p.dos[1] + (int64_t)qt * kTile * p.dos[2]) * 2), gl, wave);
+    const uint32_t soff = (uint32_t)(((int64_t)g * Tq + (int64_t)qt * kTile) * 4);
+    if (wave == 0) tiles::load_row64_f32(lsep, st_bytes, soff, sl, lane);
+    if (wave == 1) tiles::load_row64_f32(dlp, st_bytes, soff, sl + kTile, lane);
+  };
+  if (ntiles > 0) issue(0, q0, g0, st0);
+
+  bf16x8 kf[D / 16], vf[D / 16];
+  load_frags<D>(kp, p.ks[2], key, Tk, half, kf);
+  load_frags<D>(vp, p.vs[2], key, Tk, half, vf);
+
+  f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
+
+  const float sl2 = p.scale_log2;
+  const int rsw = tile_swz<D>(l32);
+  const TrReader<D> tr(lane);
+
+  // One 32-query block (tile rows mt*32 ..) against this wave's 32 keys.
+  auto block = [&](const bf16* ql, const bf16* gl, const float* sl, int g, int qb, int mt, auto edge_tag)
+      __attribute__((always_inline)) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    f32x16 s, dp;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(ql, mt, kk, l32, half, rsw), kf[kk], s, 0, 0, 0);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(gl, mt, kk, l32, half, rsw), vf[kk], dp, 0, 0, 0);
+    bf16x8 pb[2], db[2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int trow = mt * 32 + r * 8 + half * 4;  // tile row of entries 4r .. 4r+3
+      const f32x4 lse4 = *reinterpret_cast<const f32x4*>(&sl[trow]);
+      const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&sl[kTile + trow]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = r * 4 + e;
+        const int q = qb + trow + e;
+        float x = s[i] * sl2;
+        if constexpr (MASK) {
+          if (q < Tq && key < Tk)
+            x += kLog2e * load_mask(p.mask, p.mask_dtype,
+                                    b * p.ms[0] + (int64_t)(hk * G + g) * p.ms[1] + (int64_t)q * p.ms[2] +
+                                        (int64_t)key * p.ms[3]);
+        }
+        float pr = __builtin_amdgcn_exp2f(x - lse4[e]);
+        if constexpr (EDGE) {
+          if (q >= Tq || (CAUSAL && key > q)) pr = 0.f;
+        }
+        const float ds = pr * (dp[i] - dl4[e]);
+        pb[i >> 3][i & 7] = static_cast<bf16>(pr);
+        db[i >> 3][i & 7] = static_cast<bf16>(ds);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr.read(gl, mt * 2 + ks, dt), pb[ks], dv[dt], 0, 0, 0);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr.read(ql, mt * 2 + ks, dt), db[ks], dk[dt], 0, 0, 0);
+  };
+
+  auto step = [&](int t, const bf16* ql, const bf16* gl, const float* sl) __attribute__((always_inline)) {
+    const int g = tile_head(t), qb = tile_q(t) * kTile;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int q0r = qb + mt * 32;
+      if (q0r >= Tq || (CAUSAL && q0r + 31 < kw)) continue;  // no query of this block sees a key
+      const bool edge = (q0r + 32 > Tq) || (CAUSAL && q0r < kw + 31);
+      if (edge)
+        block(ql, gl, sl, g, qb, mt, std::true_type{});
+      else
+        block(ql, gl, sl, g, qb, mt, std::false_type{});
+    }
+  };
+
+  wait_dma();
+  __syncthreads();
+  for (int t = 0; t < ntiles; t += 2) {
+    if (t + 1 < ntiles) issue(t + 1, q1, g1, st1);
+    step(t, q0, g0, st0);
+    wait_dma();
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    if (t + 2 < ntiles) issue(t + 2, q0, g0, st0);
+    step(t + 1, q1, g1, st1);
+    wait_dma();
+    __syncthreads();
+  }
+
+  if (key < Tk) {
+    bf16* dko = static_cast<bf16*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + (int64_t)key * p.dks[2];
+    bf16* dvo = static_cast<bf16*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + (int64_t)key * p.dvs[2];
+    store_rowT<D>(dko, dk, half, p.scale);
+    store_rowT<D>(dvo, dv, half, 1.f);
+  }
+}
+
+// ----------------------------------------------------------------------- dQ
+
+template <int D, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 k0[kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 v0[kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 k1[kTile * D];
+  __shared__ __attribute__((aligned(16))) bf16 v1[kTile * D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int nmb = (p.Tq + kRows - 1) / kRows;
+  const int BH = p.B * p.Hq;
+  const int id = blockIdx.x;
+  int bh, mblk;
+  if ((BH & 7) == 0) {
+    // Heads dealt to the 8 XCDs round-robin, longest causal q-block first.
+    const int xcd = id & 7, slot = id >> 3, bpx = BH >> 3;
+    bh = (slot % bpx) * 8 + xcd;
+    mblk = nmb - 1 - slot / bpx;
+  } else {
+    bh = id % BH;
+    mblk = nmb - 1 - id / BH;
+  }
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h / p.group;
+  const int Tq = p.Tq, Tk = p.Tk;
+  const int q0 = mblk * kRows + wave * 32;
+  const int qi = q0 + l32;
+
+  const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+  const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+  int kv_end = Tk;
+  if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kRows));
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+  const Loader<D> kload(kp, p.ks[2], Tk, wave, lane), vload(vp, p.vs[2], Tk, wave, lane);
+  auto issue = [&](int t, bf16* kl, bf16* vl) {
+    kload.load(t, kl, wave);
+    vload.load(t, vl, wave);
+  };
+  if (ntiles > 0) issue(0, k0, v0);
+
+  bf16x8 qf[D / 16], gf[D / 16];
+  load_frags<D>(static_cast<const bf16*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], qi, Tq, half, qf);
+  load_frags<D>(static_cast<const bf16*>(p.dout) + b * p.dos[0] + h * p.dos[1], p.dos[2], qi, Tq, half, gf);
+  const int64_t row = (int64_t)bh * Tq + min(qi, Tq - 1);
+  const float lse = p.lse[row], dl = p.delta[row];
+
+  f32x16 dq[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dq[dt][i] = 0.f;
+
+  const float sl2 = p.scale_log2;
+  const int rsw = tile_swz<D>(l32);
+  const TrReader<D> tr(lane);
+
+  auto block = [&](const bf16* kl, const bf16* vl, int kb, int mt, auto edge_tag) __attribute__((always_inline)) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    f32x16 s, dp;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(kl, mt, kk, l32, half, rsw), qf[kk], s, 0, 0, 0);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(vl, mt, kk, l32, half, rsw), gf[kk], dp, 0, 0, 0);
+    bf16x8 db[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+      float x = s[i] * sl2;
+      if constexpr (MASK) {
+        if (qi < Tq && key < Tk)
+          x += kLog2e * load_mask(p.mask, p.mask_dtype,
+                                  b * p.ms[0] + (int64_t)h * p.ms[1] + (int64_t)qi * p.ms[2] +
+                                      (int64_t)key * p.ms[3]);
+      }
+      float pr = __builtin_amdgcn_exp2f(x - lse);
+      if constexpr (EDGE) {
+        if (key >= Tk || (CAUSAL && key > qi)) pr = 0.f;
+      }
+      db[i >> 3][i & 7] = static_cast<bf16>(pr * (dp[i] - dl));
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr.read(kl, mt * 2 + ks, dt), db[ks], dq[dt], 0, 0, 0);
+  };
+
+  auto step = [&](int t, const bf16* kl, const bf16* vl) __attribute__((always_inline)) {
+    const int kb = t * kTile;
+    if (q0 >= Tq) return;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int k0r = kb + mt * 32;
+      if (k0r >= Tk || (CAUSAL && k0r > q0 + 31)) continue;  // nothing of this block is visible
+      const bool edge = (k0r + 32 > Tk) || (CAUSAL && k0r + 31 > q0);
+      if (edge)
+        block(kl, vl, kb, mt, std::true_type{});
+      else
+        block(kl, vl, kb, mt, std::false_type{});
+    }
+  };
+
+  wait_dma();
+  __syncthreads();
+  for (int t = 0; t < ntiles; t += 2) {
+    if (t + 1 < ntiles) issue(t + 1, k1, v1);
+    step(t, k0, v0);
+    wait_dma();
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    if (t + 2 < ntiles) issue(t + 2, k0, v0);
+    step(t + 1, k1, v1);
+    wait_dma();
+    __syncthreads();
+  }
+
+  if (qi < Tq) {
+    bf16* dqo = static_cast<bf16*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + (int64_t)qi * p.dqs[2];
+    store_rowT<D>(dqo, dq, half, p.scale);
+  }
+}
+
+template <int D, bool CAUSAL, bool MASK>
+int launch_t(const SdpaBwdParams& p, hipStream_t s) {
+  const int64_t kv_blocks = (int64_t)p.B * p.Hkv * ((p.Tk + kRows - 1) / kRows);
+  hipLaunchKernelGGL((bwd_dkdv_mfma<D, CAUSAL, MASK>), dim3((unsigned)kv_blocks), dim3(kNT), 0, s, p);
+  if (int rc = launch_status("bwd_dkdv_mfma")) return rc;
+  const int64_t q_blocks = (int64_t)p.B * p.Hq * ((p.Tq + kRows - 1) / kRows);
+  hipLaunchKernelGGL((bwd_dq_mfma<D, CAUSAL, MASK>), dim3((unsigned)q_blocks), dim3(kNT), 0, s, p);
+  return launch_status("bwd_dq_mfma");
+}
+
+template <int D>
+int launch_d(const SdpaBwdParams& p, hipStream_t s) {
+  const bool m = p.mask != nullptr;
+  if (p.causal) return m ? launch_t<D, true, true>(p, s) : launch_t<D, true, false>(p, s);
+  return m ? launch_t<D, false, true>(p, s) : launch_t<D, false, false>(p, s);
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+}  // namespace
+
+bool bwd_mfma_supports(const SdpaBwdParams& p) {
+  if (p.dtype != MFX_BF16) return false;
+  if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
+  if (!(p.scale_log2 > 0.f)) return false;
+  const void* ptrs[7] = {p.q, p.k, p.v, p.dout, p.dq, p.dk, p.dv};
+  for (const void* ptr : ptrs)
+    if (!aligned16(ptr)) return false;
+  for (int i = 0; i < 3; ++i)
+    if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.dos[i] % 8 || p.dqs[i] % 4 || p.dks[i] % 4 ||
+        p.dvs[i] % 4)
+      return false;
+  // Buffer-resource extents are 31-bit: one kv head's K / V rows, and the
+  // query rows (and lse / delta) of all heads of one group.
+  const int64_t lim = 1LL << 31;
+  if ((int64_t)p.Tk * p.ks[2] * 2 >= lim || (int64_t)p.Tk * p.vs[2] * 2 >= lim) return false;
+  if (((int64_t)(p.group - 1) * p.qs[1] + (int64_t)p.Tq * p.qs[2] + p.D) * 2 >= lim) return false;
+  if (((int64_t)(p.group - 1) * p.dos[1] + (int64_t)p.Tq * p.dos[2] + p.D) * 2 >= lim) return false;
+  // Tile offsets in bytes stay below 2^31 as well.
+  if ((int64_t)p.qs[1] < 0 || p.qs[2] < 0 || p.dos[1] < 0 || p.dos[2] < 0) return false;
+  if ((int64_t)p.group * p.Tq * 4 >= lim) return false;
+  if ((int64_t)p.B * p.Hq * ((p.Tq + kRows - 1) / kRows) >= lim) return false;
+  return true;
+}
 
 int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s) {
-  return fail(MFX_E_UNSUPPORTED, "matrix-core backward not available");
+  if (p.D == 128) return launch_d<128>(p, s);
+  return launch_d<64>(p, s);
 }
 
 }  // namespace mfx

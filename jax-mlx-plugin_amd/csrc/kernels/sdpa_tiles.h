@@ -44,8 +44,8 @@ __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70);
 // RPI = 64 / (D/8).  Instructions NOFF apart start a swizzle period apart, so
 // they share a per-lane source offset and differ by a scalar offset: NOFF
 // VGPRs per operand, and the tile start and the step are scalar offsets.
-// The resource spans the Tk rows of this (batch, head): rows past Tk are out
-// of range and read as zeros (callers mask their scores to -inf, so they
+// The resources span the Tk rows of this (batch, head): rows past Tk are out
+// of range and read as zeros (callers also mask their scores, so they
 // contribute exactly 0).
 template <int D, int BN, int NW>
 struct TileLoader {
@@ -80,17 +80,40 @@ struct TileLoader {
   }
   // The buffer-resource type exists only for the device target; the host
   // pass of a translation unit sees an empty body.
-  __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
+  //
+  // The hardware range check covers the per-lane (VGPR) offset only, not the
+  // scalar offset, so each instruction gets a resource whose base is its
+  // first row and whose extent is what remains of the `nbytes` span from
+  // there: rows past the end then read as zeros instead of touching memory
+  // beyond the tensor.
+  __device__ __forceinline__ void load_at(uint32_t soff, bf16* lds, int wave) const {
 #if defined(__HIP_DEVICE_COMPILE__)
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, nbytes, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i)
+    for (int i = 0; i < LOADS; ++i) {
+      const uint32_t off = soff + (i / NOFF) * period_bytes;
+      const int64_t rem = (int64_t)nbytes - (int64_t)off;
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<char*>(base) + off, (short)0, rem > 0 ? (int)rem : 0, 0x00020000);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + (NW * i + wave) * 64 * 8), 16,
-                                               voff[i % NOFF],
-                                               (uint32_t)t * tile_bytes + (i / NOFF) * period_bytes, 0, 0);
+                                               voff[i % NOFF], 0, 0, 0);
+    }
 #endif
   }
+  __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
+    load_at((uint32_t)t * tile_bytes, lds, wave);
+  }
 };
+
+// 64 consecutive fp32 values (base + soff bytes onward) into LDS with one
+// 4-byte LDS-DMA load per lane; values at or past `nbytes` read as zero.
+__device__ __forceinline__ void load_row64_f32(const float* base, int nbytes, uint32_t soff, float* lds, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int64_t rem = (int64_t)nbytes - (int64_t)soff;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<char*>(const_cast<float*>(base)) + soff, (short)0, rem > 0 ? (int)rem : 0, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)lds, 4, (uint32_t)lane * 4, 0, 0, 0);
+#endif
+}
 
 }  // namespace tiles
 }  // namespace mfx

@@ -227,7 +227,7 @@ class Planner {
   static void check_supported(const Node& n) {
     static const std::set<std::string> ok = {
         "stablehlo.dot_general", "stablehlo.dot", "stablehlo.reduce", "mfx.sdpa", "mfx.layer_norm",
-        "mfx.rms_norm", "mfx.softmax", "mfx.layer_norm_bwd", "stablehlo.concatenate"};
+        "mfx.rms_norm", "mfx.softmax", "mfx.layer_norm_bwd", "mfx.sdpa_bwd", "stablehlo.concatenate"};
     if (!ok.count(n.op)) {
       std::string what = n.op;
       if (n.op == "stablehlo.custom_call") what += " @" + n.strs.at("target");
@@ -967,6 +967,78 @@ class Planner {
     io_.push_back(io);
   }
 
+  // custom_call @mlx_sdpa_bwd: BTNH (q, k, v, dO) -> (dq, dk, dv).
+  void emit_sdpa_bwd(const Node& n) {
+    const auto& sh = n.ints.at("shape");
+    const int64_t B = sh[0], N = sh[1], K = sh[2], T = sh[3], S = sh[4], H = sh[5], Hv = sh[6];
+    mfx_sdpa_bwd_args a{};
+    a.B = B;
+    a.Hq = N;
+    a.Hkv = K;
+    a.Tq = T;
+    a.Tk = S;
+    a.D = H;
+    a.Dv = Hv;
+    auto btnh = [](int64_t* st, int64_t t, int64_t heads, int64_t d) {
+      st[0] = t * heads * d;
+      st[1] = d;
+      st[2] = heads * d;
+      st[3] = 1;
+    };
+    btnh(a.q_strides, T, N, H);
+    btnh(a.dq_strides, T, N, H);
+    btnh(a.k_strides, S, K, H);
+    btnh(a.dk_strides, S, K, H);
+    btnh(a.v_strides, S, K, Hv);
+    btnh(a.dv_strides, S, K, Hv);
+    btnh(a.do_strides, T, N, Hv);
+    a.scale = (float)n.nums.at("scale");
+    const DType dt = ty(n.in[0]).dtype;
+    a.dtype = mfx_dtype(dt);
+    for (int v : n.in)
+      if (ty(v).dtype != dt) throw ParseError("mlx_sdpa_bwd operands must share one dtype");
+    for (int v : n.out)
+      if (ty(v).dtype != dt) throw ParseError("mlx_sdpa_bwd results must have the operands' dtype");
+    if (a.dtype != MFX_F32 && a.dtype != MFX_BF16) throw ParseError("mlx_sdpa_bwd: dtype must be f32 or bf16");
+    for (int i = 0; i < 4; ++i) check_dense("sdpa bwd operand", n.in[i], ty(n.in[i]).numel());
+    for (int i = 0; i < 3; ++i) check_dense("sdpa bwd result", n.out[i], ty(n.out[i]).numel());
+    mfx_sdpa_bwd_args probe = a;
+    probe.q = probe.k = probe.v = probe.dout = (void*)0x10000;
+    probe.dq = probe.dk = probe.dv = (void*)0x10000;
+    const size_t ws = mfx_sdpa_bwd_workspace_size(&probe);
+    if (!ws) throw ParseError(std::string("mlx_sdpa_bwd: ") + mfx_last_error());
+    Type wt;
+    wt.dtype = DType::kU8;
+    wt.dims = {(int64_t)ws};
+    const int ws_v = new_temp(wt);
+    const int q = n.in[0], k = n.in[1], v = n.in[2], g = n.in[3];
+    const int dq = n.out[0], dk = n.out[1], dv = n.out[2];
+    auto loc = loc_;
+    Plan* plan = &plan_;
+    Step s;
+    s.kind = "sdpa_bwd";
+    s.label = "mfx.sdpa_bwd";
+    // recomputed forward (2 products) + backward (dP, dV, dK, and S, dP, dQ)
+    s.flops = 2.0 * B * N * (double)T * S * (2 * H + 2 * Hv + 2 * H + Hv + H + Hv);
+    s.run = [a, q, k, v, g, dq, dk, dv, ws_v, ws, loc, plan](const ExecBuffers& b, std::string& err) {
+      mfx_sdpa_bwd_args r = a;
+      r.q = plan->ptr((*loc)[q], b);
+      r.k = plan->ptr((*loc)[k], b);
+      r.v = plan->ptr((*loc)[v], b);
+      r.dout = plan->ptr((*loc)[g], b);
+      r.dq = plan->ptr((*loc)[dq], b);
+      r.dk = plan->ptr((*loc)[dk], b);
+      r.dv = plan->ptr((*loc)[dv], b);
+      r.workspace = plan->ptr((*loc)[ws_v], b);
+      r.workspace_bytes = ws;
+      int rc = mfx_sdpa_bwd(&r, b.stream);
+      if (rc != MFX_OK) err = mfx_last_error();
+      return rc;
+    };
+    plan_.steps_.push_back(std::move(s));
+    io_.push_back(StepIO{{q, k, v, g}, {dq, dk, dv, ws_v}});
+  }
+
   void emit_sdpa(const Node& n) {
     const auto& sh = n.ints.at("shape");
     mfx_sdpa_args a{};
@@ -1164,6 +1236,7 @@ class Planner {
         else if (n.op == "mfx.sdpa") emit_sdpa(n);
         else if (n.op == "stablehlo.concatenate") emit_concat(n);
         else if (n.op == "mfx.layer_norm_bwd") emit_norm_bwd(n);
+        else if (n.op == "mfx.sdpa_bwd") emit_sdpa_bwd(n);
         else emit_norm(n);
         continue;
       }

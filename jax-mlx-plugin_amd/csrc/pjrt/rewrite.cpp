@@ -1191,6 +1191,34 @@ int rewrite_custom_calls(Ctx& c, RewriteStats& st) {
       st.custom_calls++;
       st.layer_norm++;
       ++count;
+    } else if (target == "mlx_sdpa_bwd") {
+      // (q, k, v, grad_out) BTNH -> (dq, dk, dv) like the operands
+      // (reference src/jax_mlx/sdpa.py:52-60, handler src/jax_mlx_pjrt.cpp:8151-8206).
+      if (n.in.size() != 4 || n.out.size() != 3)
+        throw ParseError("mlx_sdpa_bwd expects 4 operands and 3 results");
+      const Type& qt = c.ty(n.in[0]);
+      const Type& kt = c.ty(n.in[1]);
+      const Type& vt = c.ty(n.in[2]);
+      if (qt.rank() != 4 || kt.rank() != 4 || vt.rank() != 4) throw ParseError("mlx_sdpa_bwd expects rank-4 BTNH operands");
+      const int64_t B = qt.dims[0], T = qt.dims[1], N = qt.dims[2], H = qt.dims[3];
+      const int64_t S = kt.dims[1], K = kt.dims[2], Hv = vt.dims[3];
+      if (kt.dims[0] != B || kt.dims[3] != H || vt.dims[0] != B || vt.dims[1] != S || vt.dims[2] != K ||
+          K <= 0 || N % K != 0)
+        throw ParseError("mlx_sdpa_bwd operand shapes do not agree");
+      if (c.ty(n.in[3]).dims != std::vector<int64_t>{B, T, N, Hv} || c.ty(n.out[0]).dims != qt.dims ||
+          c.ty(n.out[1]).dims != kt.dims || c.ty(n.out[2]).dims != vt.dims)
+        throw ParseError("mlx_sdpa_bwd grad_out / result shapes do not agree with q, k, v");
+      double scale = 1.0;
+      json_number(cfg, "scale", scale);
+      Node f;
+      f.op = "mfx.sdpa_bwd";
+      f.in = n.in;
+      f.out = n.out;
+      f.ints["shape"] = {B, N, K, T, S, H, Hv};
+      f.nums["scale"] = scale;
+      n = f;
+      st.custom_calls++;
+      ++count;
     } else if (target == "mlx_layer_norm_bwd") {
       // (x, weight, bias, grad_out) -> (dx, dweight, dbias); bias only fixes
       // the dbias type (reference src/jax_mlx/layer_norm.py:46-56).

@@ -397,6 +397,20 @@ def custom_call_layer_norm_module(shape=(4, 512), eps=1e-5, dt="f32"):
     return module("jit_mlx_layer_norm", [f.text([o], [ty(shape, dt)])])
 
 
+def custom_call_sdpa_bwd_module(B=2, T=64, N=4, K=None, H=64, S=None, dt="f32", scale=0.125):
+    """custom_call @mlx_sdpa_bwd as emitted by the reference's lowering
+    (src/jax_mlx/sdpa.py:114-130): BTNH (q, k, v, grad_out) -> (dq, dk, dv)."""
+    K = K or N
+    S = S or T
+    qt, kt = ty([B, T, N, H], dt), ty([B, S, K, H], dt)
+    f = Fn("main", [([B, T, N, H], dt), ([B, S, K, H], dt), ([B, S, K, H], dt), ([B, T, N, H], dt)])
+    cfg = '{\\22scale\\22: ' + repr(float(scale)) + '}'
+    r = f.new()
+    f.lines.append(f'    {r}:3 = stablehlo.custom_call @mlx_sdpa_bwd(%arg0, %arg1, %arg2, %arg3) '
+                   f'{{backend_config = "{cfg}"}} : ({qt}, {kt}, {kt}, {qt}) -> ({qt}, {kt}, {kt})')
+    return module("jit_mlx_sdpa_bwd", [f.text([f"{r}#0", f"{r}#1", f"{r}#2"], [qt, kt, kt])])
+
+
 def custom_call_layer_norm_bwd_module(shape=(4, 512), eps=1e-5, dt="f32", pdt=None):
     """custom_call @mlx_layer_norm_bwd (src/jax_mlx/layer_norm.py:102-116):
     (x, weight, bias, grad_out) -> (dx, dweight, dbias)."""

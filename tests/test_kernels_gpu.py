@@ -459,3 +459,32 @@ def test_sdpa_bwd_known_answers(cuda, nat):
     dq, dk, dv = nat.sdpa_bwd(q, k, v, g)
     assert np.abs(host(dq)).max() <= 1e-5
     np.testing.assert_allclose(host(dv)[0, 0], np.tile(host(g).sum(axis=2)[0, 0] / 16, (16, 1)), atol=1e-5)
+
+
+def test_sdpa_bwd_kernel_selection(cuda, nat):
+    q, k, v = make_qkv(cuda, 1, (1, 2, 64, 128), (1, 2, 64, 128), cuda.bfloat16)
+    assert nat.sdpa_bwd_kernel_name(q, k, v) == "mfma_bf16_d128"
+    q, k, v = make_qkv(cuda, 1, (1, 2, 64, 64), (1, 2, 64, 64), cuda.bfloat16)
+    assert nat.sdpa_bwd_kernel_name(q, k, v, causal=True) == "mfma_bf16_d64"
+    q, k, v = make_qkv(cuda, 1, (1, 2, 64, 64), (1, 2, 64, 64), cuda.float32)
+    assert nat.sdpa_bwd_kernel_name(q, k, v) == "generic"
+
+
+def test_sdpa_bwd_config3_full_size(cuda, nat, oracle):
+    """Config 3 shape (bf16 [4,32,2048,128], causal): the gradients of two
+    (batch, head) pairs against the fp64 oracle run on those heads alone
+    (heads are independent), plus finiteness everywhere."""
+    q, k, v = make_qkv(cuda, 3, (4, 32, 2048, 128), (4, 32, 2048, 128), cuda.bfloat16)
+    g = dev(cuda, np.random.default_rng(103).standard_normal((4, 32, 2048, 128)), cuda.bfloat16)
+    assert nat.sdpa_bwd_kernel_name(q, k, v, causal=True) == "mfma_bf16_d128"
+    dq, dk, dv = nat.sdpa_bwd(q, k, v, g, causal=True)
+    cuda.cuda.synchronize()
+    for t in (dq, dk, dv):
+        assert bool(cuda.isfinite(t).all())
+    sc = 1.0 / np.sqrt(128)
+    for b, h in ((0, 0), (3, 31)):
+        sl = lambda t: host(t[b:b + 1, h:h + 1])
+        refs = oracle.sdpa_bwd(sl(q), sl(k), sl(v), sl(g), sc, causal=True)
+        for name, o, r in zip(("dq", "dk", "dv"), (dq, dk, dv), refs):
+            rr = rel_inf(sl(o), r)
+            assert rr <= BF16_REL_TOL, (b, h, name, rr)

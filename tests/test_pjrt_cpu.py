@@ -293,6 +293,11 @@ def test_custom_calls(api):
     (n,) = fused(d)
     assert n["op"] == "mfx.layer_norm_bwd" and math.isclose(n["f:eps"], 1e-4, rel_tol=1e-6)
     assert steps(d) == ["layer_norm_bwd"] and d["plan"]["arena_bytes"] > 0  # parameter partials
+    d = api.inspect(M.custom_call_sdpa_bwd_module(B=2, T=128, N=8, K=2, H=64, scale=0.3))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.sdpa_bwd" and n["i:shape"] == [2, 8, 2, 128, 128, 64, 64]
+    assert math.isclose(n["f:scale"], 0.3, rel_tol=1e-6)
+    assert steps(d) == ["sdpa_bwd"] and d["plan"]["arena_bytes"] > 0  # recomputed O, lse, delta
 
 
 def test_transformer_plan(api):

@@ -116,6 +116,29 @@ def test_custom_call_layer_norm_bwd(client, oracle, shape, dt, pdt):
             assert rel_inf(o, r) <= BF16_REL_TOL
 
 
+@pytest.mark.parametrize("dt,B,T,N,K,H,S", [("f32", 2, 64, 4, 4, 64, 64), ("bf16", 1, 128, 8, 2, 128, 160),
+                                             ("bf16", 2, 96, 4, 4, 64, 96)])
+def test_custom_call_sdpa_bwd(client, oracle, dt, B, T, N, K, H, S):
+    """custom_call @mlx_sdpa_bwd (reference src/jax_mlx_pjrt.cpp:8151-8206):
+    BTNH gradients against the fp64 closed form."""
+    rng = np.random.default_rng(22)
+    q = rng.standard_normal((B, T, N, H)).astype(np.float32)
+    k = rng.standard_normal((B, S, K, H)).astype(np.float32)
+    v = rng.standard_normal((B, S, K, H)).astype(np.float32)
+    g = rng.standard_normal((B, T, N, H)).astype(np.float32)
+    if dt == "bf16":
+        q, k, v, g = (bf16_round(a) for a in (q, k, v, g))
+    sc = 1.0 / np.sqrt(H)
+    outs = run(client, M.custom_call_sdpa_bwd_module(B, T, N, K, H, S, dt=dt, scale=sc), [q, k, v, g], [dt] * 4)
+    tr = lambda a: a.transpose(0, 2, 1, 3)
+    refs = [tr(r) for r in oracle.sdpa_bwd(tr(q), tr(k), tr(v), tr(g), sc)]
+    for o, r in zip(outs, refs):
+        if dt == "f32":
+            assert np.abs(o - r).max() <= F32_SDPA_TOL * max(1.0, np.abs(r).max())
+        else:
+            assert rel_inf(o, r) <= BF16_REL_TOL
+
+
 @pytest.mark.parametrize("dt,upcast", [("f32", False), ("bf16", True)])
 def test_rms_norm(client, oracle, dt, upcast):
     rng = np.random.default_rng(13)
