@@ -292,6 +292,45 @@ def bench_config4(torch, steps, warmup):
     return res
 
 
+def bench_config3_bwd(torch, native, steps, warmup):
+    """mfx_sdpa_bwd on the config-3 shape (causal bf16 [4,32,2048,128]): the
+    recomputed forward (O and lse), delta, dK/dV and dQ.  TFLOP/s uses the
+    FlashAttention-2 convention of 2.5x the forward's causal FLOPs (the five
+    backward products S, dP, dV, dQ, dK), so the recompute is overhead."""
+    import numpy as np
+
+    B, H, T, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(3)
+    q, k, v, g = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32))
+                  .to("cuda").bfloat16() for _ in range(4))
+    ws = torch.empty(native.sdpa_bwd_workspace_size(q, k, v, causal=True), dtype=torch.uint8, device="cuda")
+    fn = lambda: native.sdpa_bwd(q, k, v, g, causal=True, workspace=ws)  # noqa: E731
+    avg_ms, med_ms, _ = time_launches(torch, fn, steps, warmup)
+    flops = 2.5 * sdpa_causal_flops(B, H, T, d)
+    return {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "flops_fa2_convention": flops,
+            "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
+            "frac_bf16_peak": flops / (avg_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+            "kernel": native.sdpa_bwd_kernel_name(q, k, v, causal=True)}
+
+
+def bench_layer_norm_bwd(torch, native, rows, n, steps, warmup, seed=1):
+    """mfx_layer_norm_bwd f32: reads x and dy, writes dx (the HBM roofline's
+    bytes) plus dgamma / dbeta through per-workgroup partials."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    x = torch.from_numpy(rng.standard_normal((rows, n)).astype(np.float32)).to("cuda")
+    dy = torch.from_numpy(rng.standard_normal((rows, n)).astype(np.float32)).to("cuda")
+    gamma = torch.ones(n, device="cuda")
+    dx = torch.empty_like(x)
+    ws = torch.empty(native.layer_norm_bwd_workspace_size(x, gamma), dtype=torch.uint8, device="cuda")
+    fn = lambda: native.layer_norm_bwd(x, dy, gamma, dx=dx, workspace=ws)  # noqa: E731
+    avg_ms, med_ms, _ = time_launches(torch, fn, steps, warmup)
+    nbytes = 3.0 * rows * n * 4 + 3.0 * n * 4
+    return {"shape": [rows, n], "avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "bytes": nbytes,
+            "GBps": nbytes / (avg_ms * 1e-3) / 1e9, "frac_hbm": nbytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+
+
 def bench_copy(torch, steps, warmup, nbytes=1 << 30):
     """Plain device-to-device copy of `nbytes`: reads and writes exactly
     nbytes each, the reference point for the FETCH_SIZE / WRITE_SIZE
@@ -313,6 +352,10 @@ ONLY = {
         "sweep": [bench_layer_norm(torch, native, 1 << 20, 512, k, w),
                   bench_layer_norm(torch, native, 65536, 4096, k, w)]},
     "copy": lambda torch, native, k, w: bench_copy(torch, k, w),
+    "config3_bwd": lambda torch, native, k, w: bench_config3_bwd(torch, native, k, w),
+    "ln_bwd": lambda torch, native, k, w: {
+        "sweep": [bench_layer_norm_bwd(torch, native, 1 << 20, 512, k, w),
+                  bench_layer_norm_bwd(torch, native, 65536, 4096, k, w)]},
 }
 
 
@@ -396,6 +439,15 @@ def main() -> int:
         extra["config2_sdpa_f32"] = bench_config2(torch, native, 200, 20)
         log("config 5: GQA decode bf16 + RMSNorm(q)")
         extra["config5_decode"] = bench_config5(torch, native, 50, 5)
+        torch.cuda.empty_cache()
+        log("config 3 backward: mfx_sdpa_bwd causal bf16 [4,32,2048,128]")
+        extra["config3_sdpa_bwd"] = bench_config3_bwd(torch, native, 10, 2)
+        torch.cuda.empty_cache()
+        log("LayerNorm backward f32 HBM sweep")
+        extra["layer_norm_bwd_sweep"] = [
+            bench_layer_norm_bwd(torch, native, 1 << 20, 512, 20, 3),
+            bench_layer_norm_bwd(torch, native, 65536, 4096, 20, 3),
+        ]
         torch.cuda.empty_cache()
         log("config 4: 4-layer transformer forward through PJRT")
         extra["config4_transformer_pjrt"] = bench_config4(torch, 20, 3)

@@ -8,9 +8,10 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - delta),  delta = rowsum(dO * O)
 //   dQ = s * dS K,  dK = s * dS^T Q
 // Order of work: forward (O and lse into the workspace), delta, then dK / dV
-// and dQ.  dK / dV are owned per key row (summing the group's query heads)
-// and dQ per query row, so no output is accumulated by two workgroups and the
-// result is deterministic.
+// and dQ (the matrix-core dQ kernel computes delta itself and runs before
+// dK / dV, which read it).  dK / dV are owned per key row (summing the
+// group's query heads) and dQ per query row, so no output is accumulated by
+// two workgroups and the result is deterministic.
 //
 // The shape-general kernels here take any head size up to 256, f32 or bf16,
 // and every mask; one wavefront owns one output row and walks the other axis
@@ -328,6 +329,7 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
   else rc = launch_generic(f, s);
   if (rc != MFX_OK) return rc;
 
+  if (pl.mfma) return launch_bwd_mfma(p, s);
   const int64_t rows = (int64_t)p.B * p.Hq * p.Tq;
   const unsigned dblocks = (unsigned)((rows + 3) / 4);
   if (p.dtype == MFX_BF16)
@@ -335,8 +337,6 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
   else
     hipLaunchKernelGGL((bwd_delta_kernel<float>), dim3(dblocks), dim3(256), 0, s, p, delta);
   if ((rc = launch_status("bwd_delta_kernel")) != MFX_OK) return rc;
-
-  if (pl.mfma) return launch_bwd_mfma(p, s);
   const unsigned kv_rows = (unsigned)((int64_t)p.B * p.Hkv * p.Tk);
   if (p.dtype == MFX_BF16) {
     hipLaunchKernelGGL((bwd_dkdv_generic<bf16>), dim3(kv_rows), dim3(64), 0, s, p);

@@ -20,7 +20,8 @@
 //
 // dq: workgroup = 4 wavefronts = 128 queries of one (batch, head), each
 //   owning 32; Q and dO rows in registers, K and V stream in 64-key tiles as
-//   in the forward kernel:
+//   in the forward kernel.  It runs first and also produces each row's
+//   delta = rowsum(dO * O) for the dkdv kernel:
 //     S^T = K Q^T, dP^T = V dO^T   (lane = query: lse / delta are scalars)
 //     dQ^T += K^T dS^T             A = K^T from the transposing LDS read
 //
@@ -314,7 +315,24 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
   load_frags<D>(static_cast<const bf16*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], qi, Tq, half, qf);
   load_frags<D>(static_cast<const bf16*>(p.dout) + b * p.dos[0] + h * p.dos[1], p.dos[2], qi, Tq, half, gf);
   const int64_t row = (int64_t)bh * Tq + min(qi, Tq - 1);
-  const float lse = p.lse[row], dl = p.delta[row];
+  const float lse = p.lse[row];
+  // delta = rowsum(dO * O): this lane's 64 features, then its partner's.
+  float dl;
+  {
+    bf16x8 of[D / 16];
+    load_frags<D>(static_cast<const bf16*>(p.o) + (int64_t)bh * Tq * D, D, qi, Tq, half, of);
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        a0 = fmaf(static_cast<float>(gf[kk][e]), static_cast<float>(of[kk][e]), a0);
+        a1 = fmaf(static_cast<float>(gf[kk][e + 1]), static_cast<float>(of[kk][e + 1]), a1);
+      }
+    dl = a0 + a1;
+    dl += __shfl_xor(dl, 32, 64);
+  }
+  if (half == 0 && qi < Tq) p.delta[row] = dl;
 
   f32x16 dq[D / 32];
 #pragma unroll
@@ -398,12 +416,12 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
 
 template <int D, bool CAUSAL, bool MASK>
 int launch_t(const SdpaBwdParams& p, hipStream_t s) {
-  const int64_t kv_blocks = (int64_t)p.B * p.Hkv * ((p.Tk + kRows - 1) / kRows);
-  hipLaunchKernelGGL((bwd_dkdv_mfma<D, CAUSAL, MASK>), dim3((unsigned)kv_blocks), dim3(kNT), 0, s, p);
-  if (int rc = launch_status("bwd_dkdv_mfma")) return rc;
   const int64_t q_blocks = (int64_t)p.B * p.Hq * ((p.Tq + kRows - 1) / kRows);
   hipLaunchKernelGGL((bwd_dq_mfma<D, CAUSAL, MASK>), dim3((unsigned)q_blocks), dim3(kNT), 0, s, p);
-  return launch_status("bwd_dq_mfma");
+  if (int rc = launch_status("bwd_dq_mfma")) return rc;
+  const int64_t kv_blocks = (int64_t)p.B * p.Hkv * ((p.Tk + kRows - 1) / kRows);
+  hipLaunchKernelGGL((bwd_dkdv_mfma<D, CAUSAL, MASK>), dim3((unsigned)kv_blocks), dim3(kNT), 0, s, p);
+  return launch_status("bwd_dkdv_mfma");
 }
 
 template <int D>

@@ -44,7 +44,7 @@ struct SdpaBwdParams {
   void* dk;
   void* dv;
   const float* lse;
-  const float* delta;
+  float* delta;  // written by the delta pass or by the matrix-core dQ kernel
   int64_t qs[4], ks[4], vs[4], dos[4], dqs[4], dks[4], dvs[4], ms[4];
   int B, Hq, Hkv, Tq, Tk, D, Dv;
   int group;
@@ -56,7 +56,8 @@ struct SdpaBwdParams {
 };
 
 bool bwd_mfma_supports(const SdpaBwdParams& p);
-int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s);  // dQ, dK, dV
+// dQ (which also computes delta from O and dO), then dK and dV.
+int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s);
 
 // Kernel families; each returns MFX_OK or an error code after launching.
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s);
