@@ -53,63 +53,105 @@ __device__ __forceinline__ float nan_min(float a, float b) {
   return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b);
 }
 
-__device__ __forceinline__ float apply(const mfx_ew_instr& in, const float* r, int64_t idx_unused) {
-  const float a = r[in.a];
+// Result of one arithmetic instruction for NV elements; opnd(e, k) is operand
+// k (0: a, 1: b, 2: c) of element e.  The switch on the (uniform) opcode
+// runs once for all NV elements.
+#define MFX_EW_UN(expr)                    \
+  _Pragma("unroll") for (int e = 0; e < NV; ++e) { \
+    const float a = opnd(e, 0);            \
+    v[e] = (expr);                         \
+  }                                        \
+  return;
+#define MFX_EW_BIN(expr)                   \
+  _Pragma("unroll") for (int e = 0; e < NV; ++e) { \
+    const float a = opnd(e, 0), b = opnd(e, 1); \
+    v[e] = (expr);                         \
+  }                                        \
+  return;
+// Library math (tens of instructions each) runs as a rolled loop so the
+// kernel keeps one copy of it.
+#define MFX_EW_UN_SLOW(expr)               \
+  _Pragma("nounroll") for (int e = 0; e < NV; ++e) { \
+    const float a = opnd(e, 0);            \
+    v[e] = (expr);                         \
+  }                                        \
+  return;
+#define MFX_EW_BIN_SLOW(expr)              \
+  _Pragma("nounroll") for (int e = 0; e < NV; ++e) { \
+    const float a = opnd(e, 0), b = opnd(e, 1); \
+    v[e] = (expr);                         \
+  }                                        \
+  return;
+#define MFX_EW_TER(expr)                   \
+  _Pragma("unroll") for (int e = 0; e < NV; ++e) { \
+    const float a = opnd(e, 0), b = opnd(e, 1), c = opnd(e, 2); \
+    v[e] = (expr);                         \
+  }                                        \
+  return;
+
+template <int NV, typename Opnd>
+__device__ __forceinline__ void apply_n(const mfx_ew_instr& in, Opnd&& opnd, float* v) {
   const bool is_int = in.flags & MFX_EW_FLAG_INT;
   switch (in.op) {
-    case MFX_EW_NEG: return -a;
-    case MFX_EW_ABS: return fabsf(a);
-    case MFX_EW_EXP: return expf(a);
-    case MFX_EW_EXPM1: return expm1f(a);
-    case MFX_EW_LOG: return logf(a);
-    case MFX_EW_LOG1P: return log1pf(a);
-    case MFX_EW_SQRT: return sqrtf(a);
-    case MFX_EW_RSQRT: return 1.0f / sqrtf(a);
-    case MFX_EW_TANH: return tanhf(a);
-    case MFX_EW_LOGISTIC: return 1.0f / (1.0f + expf(-a));
-    case MFX_EW_ERF: return erff(a);
-    case MFX_EW_SIN: return sinf(a);
-    case MFX_EW_COS: return cosf(a);
-    case MFX_EW_FLOOR: return floorf(a);
-    case MFX_EW_CEIL: return ceilf(a);
-    case MFX_EW_ROUND_NE: return rintf(a);
-    case MFX_EW_SIGN: return a > 0.f ? 1.f : (a < 0.f ? -1.f : a);
-    case MFX_EW_NOT: return is_int ? (float)(~(int32_t)a) : (a == 0.f ? 1.f : 0.f);
-    case MFX_EW_ROUND_BF16: return static_cast<float>(static_cast<bf16>(a));
-    case MFX_EW_ROUND_F16: return static_cast<float>(static_cast<_Float16>(a));
-    case MFX_EW_TO_INT: return truncf(a);
-    case MFX_EW_IS_FINITE: return isfinite(a) ? 1.f : 0.f;
-    case MFX_EW_COPY: return a;
-    default: break;
+    case MFX_EW_NEG: MFX_EW_UN(-a)
+    case MFX_EW_ABS: MFX_EW_UN(fabsf(a))
+    case MFX_EW_EXP: MFX_EW_UN_SLOW(expf(a))
+    case MFX_EW_EXPM1: MFX_EW_UN_SLOW(expm1f(a))
+    case MFX_EW_LOG: MFX_EW_UN_SLOW(logf(a))
+    case MFX_EW_LOG1P: MFX_EW_UN_SLOW(log1pf(a))
+    case MFX_EW_SQRT: MFX_EW_UN(sqrtf(a))
+    case MFX_EW_RSQRT: MFX_EW_UN(1.0f / sqrtf(a))
+    case MFX_EW_TANH: MFX_EW_UN_SLOW(tanhf(a))
+    case MFX_EW_LOGISTIC: MFX_EW_UN_SLOW(1.0f / (1.0f + expf(-a)))
+    case MFX_EW_ERF: MFX_EW_UN_SLOW(erff(a))
+    case MFX_EW_SIN: MFX_EW_UN_SLOW(sinf(a))
+    case MFX_EW_COS: MFX_EW_UN_SLOW(cosf(a))
+    case MFX_EW_FLOOR: MFX_EW_UN(floorf(a))
+    case MFX_EW_CEIL: MFX_EW_UN(ceilf(a))
+    case MFX_EW_ROUND_NE: MFX_EW_UN(rintf(a))
+    case MFX_EW_SIGN: MFX_EW_UN(a > 0.f ? 1.f : (a < 0.f ? -1.f : a))
+    case MFX_EW_NOT: MFX_EW_UN(is_int ? (float)(~(int32_t)a) : (a == 0.f ? 1.f : 0.f))
+    case MFX_EW_ROUND_BF16: MFX_EW_UN(static_cast<float>(static_cast<bf16>(a)))
+    case MFX_EW_ROUND_F16: MFX_EW_UN(static_cast<float>(static_cast<_Float16>(a)))
+    case MFX_EW_TO_INT: MFX_EW_UN(truncf(a))
+    case MFX_EW_IS_FINITE: MFX_EW_UN(isfinite(a) ? 1.f : 0.f)
+    case MFX_EW_COPY: MFX_EW_UN(a)
+    case MFX_EW_ADD: MFX_EW_BIN(a + b)
+    case MFX_EW_SUB: MFX_EW_BIN(a - b)
+    case MFX_EW_MUL: MFX_EW_BIN(a * b)
+    case MFX_EW_DIV: MFX_EW_BIN(is_int ? truncf(a / b) : a / b)
+    case MFX_EW_MAX: MFX_EW_BIN(nan_max(a, b))
+    case MFX_EW_MIN: MFX_EW_BIN(nan_min(a, b))
+    case MFX_EW_POW: MFX_EW_BIN_SLOW(powf(a, b))
+    case MFX_EW_REM: MFX_EW_BIN_SLOW(fmodf(a, b))
+    case MFX_EW_AND: MFX_EW_BIN(is_int ? (float)((int32_t)a & (int32_t)b) : ((a != 0.f && b != 0.f) ? 1.f : 0.f))
+    case MFX_EW_OR: MFX_EW_BIN(is_int ? (float)((int32_t)a | (int32_t)b) : ((a != 0.f || b != 0.f) ? 1.f : 0.f))
+    case MFX_EW_XOR: MFX_EW_BIN(is_int ? (float)((int32_t)a ^ (int32_t)b) : (((a != 0.f) != (b != 0.f)) ? 1.f : 0.f))
+    case MFX_EW_EQ: MFX_EW_BIN(a == b ? 1.f : 0.f)
+    case MFX_EW_NE: MFX_EW_BIN(a != b ? 1.f : 0.f)
+    case MFX_EW_LT: MFX_EW_BIN(a < b ? 1.f : 0.f)
+    case MFX_EW_LE: MFX_EW_BIN(a <= b ? 1.f : 0.f)
+    case MFX_EW_GT: MFX_EW_BIN(a > b ? 1.f : 0.f)
+    case MFX_EW_GE: MFX_EW_BIN(a >= b ? 1.f : 0.f)
+    case MFX_EW_ATAN2: MFX_EW_BIN_SLOW(atan2f(a, b))
+    case MFX_EW_SELECT: MFX_EW_TER(a != 0.f ? b : c)
+    case MFX_EW_CLAMP: MFX_EW_TER(nan_min(nan_max(b, a), c))
+    default:
+#pragma unroll
+      for (int e = 0; e < NV; ++e) v[e] = 0.f;
+      return;
   }
-  const float b = r[in.b];
-  switch (in.op) {
-    case MFX_EW_ADD: return a + b;
-    case MFX_EW_SUB: return a - b;
-    case MFX_EW_MUL: return a * b;
-    case MFX_EW_DIV: return is_int ? truncf(a / b) : a / b;
-    case MFX_EW_MAX: return nan_max(a, b);
-    case MFX_EW_MIN: return nan_min(a, b);
-    case MFX_EW_POW: return powf(a, b);
-    case MFX_EW_REM: return fmodf(a, b);
-    case MFX_EW_AND: return is_int ? (float)((int32_t)a & (int32_t)b) : ((a != 0.f && b != 0.f) ? 1.f : 0.f);
-    case MFX_EW_OR: return is_int ? (float)((int32_t)a | (int32_t)b) : ((a != 0.f || b != 0.f) ? 1.f : 0.f);
-    case MFX_EW_XOR: return is_int ? (float)((int32_t)a ^ (int32_t)b) : (((a != 0.f) != (b != 0.f)) ? 1.f : 0.f);
-    case MFX_EW_EQ: return a == b ? 1.f : 0.f;
-    case MFX_EW_NE: return a != b ? 1.f : 0.f;
-    case MFX_EW_LT: return a < b ? 1.f : 0.f;
-    case MFX_EW_LE: return a <= b ? 1.f : 0.f;
-    case MFX_EW_GT: return a > b ? 1.f : 0.f;
-    case MFX_EW_GE: return a >= b ? 1.f : 0.f;
-    case MFX_EW_ATAN2: return atan2f(a, b);
-    default: break;
-  }
-  const float c = r[in.c];
-  switch (in.op) {
-    case MFX_EW_SELECT: return a != 0.f ? b : c;
-    case MFX_EW_CLAMP: return nan_min(nan_max(b, a), c);
-    default: return 0.f;
-  }
+}
+#undef MFX_EW_UN
+#undef MFX_EW_BIN
+#undef MFX_EW_TER
+#undef MFX_EW_UN_SLOW
+#undef MFX_EW_BIN_SLOW
+
+__device__ __forceinline__ float apply(const mfx_ew_instr& in, const float* r) {
+  float v;
+  apply_n<1>(in, [&](int, int k) { return r[k == 0 ? in.a : k == 1 ? in.b : in.c]; }, &v);
+  return v;
 }
 
 template <typename IDX>
@@ -139,7 +181,7 @@ __global__ __launch_bounds__(kThreads) void ew_kernel(const mfx_ew_program prog,
       } else if (in.op == MFX_EW_IOTA) {
         v = (float)coord[in.a];
       } else {
-        v = apply(in, r, 0);
+        v = apply(in, r);
       }
       r[in.dst] = v;
     }
@@ -149,6 +191,132 @@ __global__ __launch_bounds__(kThreads) void ew_kernel(const mfx_ew_program prog,
       for (int d = 0; d < prog.rank; ++d) out_off += (int64_t)coord[d] * prog.out_strides[d];
     }
     store_elem(prog.out, prog.out_dtype, out_off, r[prog.result]);
+  }
+}
+
+// Four consecutive elements of the innermost (collapsed) dim per thread and
+// iteration: the output coordinates are decomposed once per four elements,
+// each instruction is decoded once per four elements, and the loads and the
+// store move four elements per instruction where the layout allows.  Input
+// i's access mode is two bits of `modes`: 0 = contiguous along the inner dim
+// and aligned for a vector load of its dtype, 1 = inner stride 0 (one value
+// for all four), 2 = anything else (four scalar loads).  The output is
+// contiguous, its inner dim a multiple of four and its pointer aligned for a
+// four-element store.
+constexpr int kV = 4;
+
+// Inputs of the four-wide kernel are f32 or bf16 (checked on the host).
+__device__ __forceinline__ void load4(const void* p, int dt, int64_t off, int64_t step, int mode, float* v) {
+  if (dt == MFX_F32) {
+    const float* f = static_cast<const float*>(p) + off;
+    if (mode == 0) {
+      const float4 w = *reinterpret_cast<const float4*>(f);
+      v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+    } else if (mode == 1) {
+      v[0] = v[1] = v[2] = v[3] = f[0];
+    } else {
+#pragma unroll
+      for (int e = 0; e < kV; ++e) v[e] = f[e * step];
+    }
+    return;
+  }
+  const bf16* h = static_cast<const bf16*>(p) + off;
+  if (mode == 0) {
+    const uint2 w = *reinterpret_cast<const uint2*>(h);
+    v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
+    v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
+  } else if (mode == 1) {
+    v[0] = v[1] = v[2] = v[3] = static_cast<float>(h[0]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kV; ++e) v[e] = static_cast<float>(h[e * step]);
+  }
+}
+
+// Output of the four-wide kernel is f32 or bf16 (checked on the host).
+__device__ __forceinline__ void store4(void* p, int dt, int64_t off, const float* v) {
+  if (dt == MFX_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + off) = make_float4(v[0], v[1], v[2], v[3]);
+    return;
+  }
+  bf16x4 w;
+#pragma unroll
+  for (int e = 0; e < kV; ++e) w[e] = static_cast<bf16>(v[e]);
+  *reinterpret_cast<bf16x4*>(static_cast<bf16*>(p) + off) = w;
+}
+
+// The program's registers live in LDS, one 16-byte slot (four elements) per
+// thread and register: lds[reg][thread] as float4, so every operand read and
+// result write is one conflict-free ds_read_b128 / ds_write_b128 whose
+// address is the thread's slot plus a uniform register offset.  (A register
+// file indexed by a runtime register number cannot stay in VGPRs: the
+// compiler lowers such accesses to select chains or scratch memory.)
+template <typename IDX, int NREG>
+__global__ __launch_bounds__(kThreads) void ew_kernel_v4(const mfx_ew_program prog, IDX nchunks, IDX inner_chunks,
+                                                         uint32_t modes) {
+  __shared__ float4 regs[NREG][kThreads];
+  float4* mine = &regs[0][threadIdx.x];
+  auto rd = [&](int i) __attribute__((always_inline)) { return mine[i * kThreads]; };
+  auto wr = [&](int i, const float* v) __attribute__((always_inline)) {
+    mine[i * kThreads] = make_float4(v[0], v[1], v[2], v[3]);
+  };
+  const int last = prog.rank - 1;
+  for (IDX c = (IDX)blockIdx.x * kThreads + threadIdx.x; c < nchunks; c += (IDX)gridDim.x * kThreads) {
+    IDX here[MFX_MAX_RANK];
+    {
+      const IDX outer = c / inner_chunks;
+      IDX rem = outer;
+      for (int d = last - 1; d >= 0; --d) {
+        const IDX n = (IDX)prog.dims[d];
+        here[d] = rem % n;
+        rem /= n;
+      }
+      here[last] = (c - outer * inner_chunks) * kV;
+    }
+    // Every input is loaded before the program runs, so all loads of a
+    // chunk are in flight together.
+    float li[MFX_EW_MAX_INPUTS][kV];
+#pragma unroll
+    for (int i = 0; i < MFX_EW_MAX_INPUTS; ++i) {
+      if (i < prog.num_inputs) {
+        const mfx_ew_input& src = prog.inputs[i];
+        int64_t off = 0;
+        for (int d = 0; d <= last; ++d) off += (int64_t)here[d] * src.strides[d];
+        load4(src.data, src.dtype, off, src.strides[last], (modes >> (2 * i)) & 3, li[i]);
+      }
+    }
+    for (int pc = 0; pc < prog.num_instrs; ++pc) {
+      const mfx_ew_instr in = prog.code[pc];
+      float v[kV];
+      if (in.op == MFX_EW_LOAD) {
+        // Uniform branch on the input index keeps li in fixed registers.
+#pragma unroll
+        for (int i = 0; i < MFX_EW_MAX_INPUTS; ++i)
+          if (in.a == i) {
+#pragma unroll
+            for (int e = 0; e < kV; ++e) v[e] = li[i][e];
+          }
+      } else if (in.op == MFX_EW_CONST) {
+        v[0] = v[1] = v[2] = v[3] = in.imm;
+      } else if (in.op == MFX_EW_IOTA) {
+        const float base = (float)here[in.a];
+#pragma unroll
+        for (int e = 0; e < kV; ++e) v[e] = in.a == last ? base + (float)e : base;
+      } else {
+        const float4 a = rd(in.a);
+        const float4 b = in.op > MFX_EW_COPY ? rd(in.b) : a;
+        const float4 cc = in.op > MFX_EW_ATAN2 ? rd(in.c) : a;
+        const float av[kV] = {a.x, a.y, a.z, a.w}, bv[kV] = {b.x, b.y, b.z, b.w}, cv[kV] = {cc.x, cc.y, cc.z, cc.w};
+        auto opnd = [&](int e, int k) __attribute__((always_inline)) {
+          return k == 0 ? av[e] : k == 1 ? bv[e] : cv[e];
+        };
+        apply_n<kV>(in, opnd, v);
+      }
+      wr(in.dst, v);
+    }
+    const float4 r = rd(prog.result);
+    const float o[kV] = {r.x, r.y, r.z, r.w};
+    store4(prog.out, prog.out_dtype, (int64_t)c * kV, o);
   }
 }
 
@@ -244,6 +412,16 @@ __global__ __launch_bounds__(kThreads) void reduce_block_kernel(
 
 bool valid_dtype(int dt) { return dt >= MFX_F32 && dt <= MFX_F64; }
 
+int dtype_bytes_of(int dt) {
+  switch (dt) {
+    case MFX_F32: case MFX_I32: case MFX_U32: return 4;
+    case MFX_BF16: case MFX_F16: return 2;
+    case MFX_PRED: case MFX_U8: case MFX_I8: return 1;
+    case MFX_I64: case MFX_F64: return 8;
+    default: return 0;
+  }
+}
+
 // Merges adjacent output dims whose strides allow it for every input.
 void collapse(mfx_ew_program& p) {
   if (p.rank <= 1) return;
@@ -311,9 +489,59 @@ int mfx_elementwise(const mfx_ew_program* prog_in, void* stream) {
   } else {
     collapse(p);
   }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Four elements per thread when the output is contiguous with an inner
+  // dim that is a multiple of four.
+  const int last = p.rank - 1;
+  const int osz = dtype_bytes_of(p.out_dtype);
+  bool fp_only = p.out_dtype == MFX_F32 || p.out_dtype == MFX_BF16;
+  for (int i = 0; i < p.num_inputs; ++i)
+    fp_only = fp_only && (p.inputs[i].dtype == MFX_F32 || p.inputs[i].dtype == MFX_BF16);
+  if (fp_only && !strided && p.rank >= 1 && p.dims[last] % kV == 0 && osz > 0 &&
+      (uintptr_t)p.out % (size_t)(osz * kV > 16 ? 16 : osz * kV) == 0) {
+    uint32_t modes = 0;
+    for (int i = 0; i < p.num_inputs; ++i) {
+      const mfx_ew_input& in = p.inputs[i];
+      const int isz = dtype_bytes_of(in.dtype);
+      int mode = 2;
+      if (in.strides[last] == 0) {
+        mode = 1;
+      } else if (in.strides[last] == 1) {
+        bool aligned = (uintptr_t)in.data % (size_t)(isz * kV) == 0;
+        for (int d = 0; d < last; ++d) aligned = aligned && in.strides[d] % kV == 0;
+        if (aligned) mode = 0;
+      }
+      modes |= (uint32_t)mode << (2 * i);
+    }
+    const int64_t chunks = numel / kV;
+    const int64_t inner_chunks = p.dims[last] / kV;
+    int nreg = p.result + 1;
+    for (int pc = 0; pc < p.num_instrs; ++pc) nreg = nreg > p.code[pc].dst + 1 ? nreg : p.code[pc].dst + 1;
+    // One chunk per thread (up to 2^24 workgroups, then a grid-stride loop).
+    const int64_t b64 = (chunks + kThreads - 1) / kThreads;
+    const unsigned g = (unsigned)(b64 < (1 << 24) ? b64 : (1 << 24));
+    const bool small = numel < (1LL << 31);
+#define MFX_EW_V4(N)                                                                                      \
+    if (small)                                                                                            \
+      hipLaunchKernelGGL((ew_kernel_v4<int32_t, N>), dim3(g), dim3(kThreads), 0, s, p, (int32_t)chunks,   \
+                         (int32_t)inner_chunks, modes);                                                  \
+    else                                                                                                  \
+      hipLaunchKernelGGL((ew_kernel_v4<int64_t, N>), dim3(g), dim3(kThreads), 0, s, p, chunks,           \
+                         inner_chunks, modes);
+    if (nreg <= 4) {
+      MFX_EW_V4(4)
+    } else if (nreg <= 8) {
+      MFX_EW_V4(8)
+    } else if (nreg <= 16) {
+      MFX_EW_V4(16)
+    } else {
+      MFX_EW_V4(MFX_EW_MAX_REGS)
+    }
+#undef MFX_EW_V4
+    return launch_status("ew_kernel_v4");
+  }
   const int64_t blocks64 = (numel + kThreads - 1) / kThreads;
   const unsigned blocks = (unsigned)(blocks64 < 65536 ? blocks64 : 65536);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (numel < (1LL << 31))
     hipLaunchKernelGGL((ew_kernel<int32_t>), dim3(blocks), dim3(kThreads), 0, s, p, (int32_t)numel, strided);
   else

@@ -429,6 +429,28 @@ def custom_call_layer_norm_bwd_module(shape=(4, 512), eps=1e-5, dt="f32", pdt=No
 
 # ---------------------------------------------------------------- transformer
 
+def elementwise_mix_module(R=64, C=256, dt="f32"):
+    """A generic-op region the fused kernels do not cover: bias add through a
+    broadcast, the tanh GELU, a product with a transposed operand, and an
+    iota / compare / select lower-triangle mask -- one elementwise program."""
+    f = Fn("main", [([R, C], dt), ([C], dt), ([C, R], dt)])
+    shape = [R, C]
+    u = f.binary("add", f.arg(0), f.bcast(f.arg(1), [C], [1], shape, dt), shape, dt)
+    u3 = f.binary("multiply", f.binary("multiply", u, u, shape, dt), u, shape, dt)
+    inner = f.binary("add", u, f.binary("multiply", f.splat(0.044715, shape, dt), u3, shape, dt), shape, dt)
+    inner = f.binary("multiply", f.splat(math.sqrt(2 / math.pi), shape, dt), inner, shape, dt)
+    t = f.binary("add", f.splat(1.0, shape, dt), f.unary("tanh", inner, shape, dt), shape, dt)
+    g = f.binary("multiply", f.binary("multiply", f.splat(0.5, shape, dt), u, shape, dt), t, shape, dt)
+    at, _ = f.transpose(f.arg(2), [C, R], [1, 0], dt)
+    y = f.binary("multiply", g, at, shape, dt)
+    i0 = f.emit(f"stablehlo.iota dim = 0 : {ty(shape, 'i32')}")
+    i1 = f.emit(f"stablehlo.iota dim = 1 : {ty(shape, 'i32')}")
+    tri = f.emit(f"stablehlo.compare  GE, {i0}, {i1},  SIGNED : ({ty(shape, 'i32')}, {ty(shape, 'i32')}) -> "
+                 f"{ty(shape, 'i1')}")
+    o = f.emit(f"stablehlo.select {tri}, {y}, {f.splat(-1.0, shape, dt)} : {ty(shape, 'i1')}, {ty(shape, dt)}")
+    return module("jit_elementwise_mix", [f.text([o], [ty(shape, dt)])])
+
+
 def transformer_module(layers=4, B=32, T=256, d=512, heads=8, mlp=2048, eps=1e-5, dt="f32", causal=False):
     """Pre-LN transformer forward (Flax-style modules under jax.jit):
     x + Attn(LN(x)); x + MLP(LN(x)) with a fused QKV projection split by

@@ -255,6 +255,32 @@ def test_gqa_decode_with_q_rms(client, oracle, S):
     assert rel_inf(o, ref) <= BF16_REL_TOL
 
 
+# ------------------------------------------------------ generic elementwise
+
+@pytest.mark.parametrize("R,C,dt", [(64, 256, "f32"), (33, 77, "f32"), (8, 1024, "bf16"), (5, 12, "bf16"),
+                                    (1000, 2048, "f32")])
+def test_elementwise_program(client, R, C, dt):
+    """One fused elementwise program (broadcast, GELU, transposed operand,
+    iota mask) against numpy in fp64.  f32: max-abs <= 1e-5 * max(1, |ref|);
+    bf16 (rounded after every op, as the module's bf16 types say): the bf16
+    relative bar.  Inner dims that are multiples of four take the four-wide
+    interpreter, the others the scalar one."""
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((R, C)).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    a = rng.standard_normal((C, R)).astype(np.float32)
+    if dt == "bf16":
+        x, b, a = (bf16_round(t) for t in (x, b, a))
+    (o,) = run(client, M.elementwise_mix_module(R, C, dt), [x, b, a], [dt] * 3)
+    u = x.astype(np.float64) + b.astype(np.float64)
+    g = 0.5 * u * (1 + np.tanh(math.sqrt(2 / math.pi) * (u + 0.044715 * u ** 3)))
+    ref = np.where(np.arange(R)[:, None] >= np.arange(C)[None, :], g * a.T.astype(np.float64), -1.0)
+    if dt == "f32":
+        assert np.abs(o - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    else:
+        assert rel_inf(o, ref) <= BF16_REL_TOL
+
+
 # ---------------------------------------------------------------- transformer
 
 def transformer_ref(oracle, x, params, heads, eps=1e-5):
