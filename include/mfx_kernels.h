@@ -88,6 +88,14 @@ int mfx_rms_norm(const mfx_norm_args* args, void* stream);
 int mfx_softmax(const mfx_norm_args* args, void* stream);
 
 /*
+ * Row log-softmax over the last axis, y = (x - max) - log(sum(exp(x - max))),
+ * same layout rules as mfx_softmax.  Replaces the reference's special-cased
+ * callee @log_softmax (src/jax_mlx_pjrt.cpp:5624-5641, an mlx max / exp /
+ * sum / log composition) for jax.nn.log_softmax's lowering.
+ */
+int mfx_log_softmax(const mfx_norm_args* args, void* stream);
+
+/*
  * LayerNorm backward over the last axis of [rows, n] views (feature stride 1,
  * one row stride per tensor), for y = (x - mean) / sqrt(var + eps) * gamma + b
  * with the population variance:

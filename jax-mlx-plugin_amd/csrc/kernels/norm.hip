@@ -13,7 +13,9 @@ namespace {
 
 using namespace rowvec;
 
-enum class RowOp { kLayerNorm, kRmsNorm, kSoftmax };
+enum class RowOp { kLayerNorm, kRmsNorm, kSoftmax, kLogSoftmax };
+
+constexpr bool is_softmax(RowOp op) { return op == RowOp::kSoftmax || op == RowOp::kLogSoftmax; }
 
 // One row per LANES threads (16 or 64 lanes of one wavefront, or a whole
 // 256-thread workgroup).  Each lane loads NV 16-byte vectors with consecutive
@@ -31,7 +33,7 @@ __global__ __launch_bounds__(kBlock) void row_kernel(
   constexpr int VEC = Vec16<T>::N;
   typedef typename Vec16<T>::type V;
   constexpr int ROWS_PER_BLOCK = kBlock / LANES;
-  constexpr bool kParams = OP != RowOp::kSoftmax;
+  constexpr bool kParams = !is_softmax(OP);
   __shared__ float lds[kBlock / 64];
 
   const int lane = threadIdx.x % LANES;
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(kBlock) void row_kernel(
       unpack16<T>(xr[vi], v[i]);
     } else {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) v[i][j] = (OP == RowOp::kSoftmax) ? -INFINITY : 0.f;
+      for (int j = 0; j < VEC; ++j) v[i][j] = is_softmax(OP) ? -INFINITY : 0.f;
     }
   }
   float gv[kParams ? NV : 1][VEC], bv[kParams && OP == RowOp::kLayerNorm ? NV : 1][VEC];
@@ -111,11 +113,13 @@ __global__ __launch_bounds__(kBlock) void row_kernel(
     for (int i = 0; i < NV; ++i)
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        v[i][j] = __expf(v[i][j] - m);
-        s += v[i][j];
+        const float e = __expf(v[i][j] - m);
+        if constexpr (OP == RowOp::kSoftmax) v[i][j] = e;
+        s += e;
       }
     s = row_reduce<LANES, false>(s, lds);
-    scale_or_max = 1.0f / s;
+    // softmax: 1 / sum;  log-softmax: the total shift max + log(sum).
+    scale_or_max = OP == RowOp::kSoftmax ? 1.0f / s : m + logf(s);
   }
 
   if (!row_ok) return;
@@ -129,6 +133,8 @@ __global__ __launch_bounds__(kBlock) void row_kernel(
     for (int j = 0; j < VEC; ++j) {
       if constexpr (OP == RowOp::kSoftmax) {
         o[j] = v[i][j] * scale_or_max;
+      } else if constexpr (OP == RowOp::kLogSoftmax) {
+        o[j] = v[i][j] - scale_or_max;
       } else if constexpr (OP == RowOp::kLayerNorm) {
         o[j] = fmaf((v[i][j] - shift) * scale_or_max, gv[i][j], bv[i][j]);
       } else {
@@ -177,13 +183,15 @@ __global__ __launch_bounds__(kBlock) void row_kernel_looped(
     float s = 0.f;
     for (int64_t i = threadIdx.x; i < n; i += kBlock) s += __expf(to_f32(xr[i]) - m);
     s = row_reduce<kBlock, false>(s, lds);
-    a = 1.0f / s;
+    a = OP == RowOp::kSoftmax ? 1.0f / s : logf(s);
     b = m;
   }
   for (int64_t i = threadIdx.x; i < n; i += kBlock) {
     float t = to_f32(xr[i]);
     if constexpr (OP == RowOp::kSoftmax) {
       t = __expf(t - b) * a;
+    } else if constexpr (OP == RowOp::kLogSoftmax) {
+      t = t - (b + a);
     } else {
       t = (t - b) * a;
       if (gamma) t *= load_param(gamma, pdt, (int)i);
@@ -219,7 +227,7 @@ int dispatch_vec(const mfx_norm_args& a, hipStream_t s, int64_t nvec) {
 template <typename T, RowOp OP>
 int dispatch_typed(const mfx_norm_args& a, hipStream_t s) {
   constexpr int VEC = Vec16<T>::N;
-  const bool params = OP != RowOp::kSoftmax && (a.gamma || (OP == RowOp::kLayerNorm && a.beta));
+  const bool params = !is_softmax(OP) && (a.gamma || (OP == RowOp::kLayerNorm && a.beta));
   // Parameter vectors are read at element offsets that are multiples of VEC.
   const int pbytes = a.param_dtype == MFX_F32 ? 4 : 2;
   const bool params_aligned = !params || ((!a.gamma || (uintptr_t)a.gamma % (VEC * pbytes > 16 ? 16 : VEC * pbytes) == 0) &&
@@ -250,7 +258,7 @@ int dispatch(const mfx_norm_args* a, void* stream) {
   if (a->n > 0x7fffffffLL) return fail(MFX_E_UNSUPPORTED, "row too long");
   if ((a->gamma || a->beta) && a->param_dtype != MFX_F32 && a->param_dtype != MFX_BF16)
     return fail(MFX_E_UNSUPPORTED, "param_dtype must be f32 or bf16");
-  if (OP != RowOp::kSoftmax && !(a->eps >= 0.f))
+  if (!is_softmax(OP) && !(a->eps >= 0.f))
     return fail(MFX_E_INVALID, "eps must be >= 0");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (a->dtype) {
@@ -275,6 +283,10 @@ int mfx_rms_norm(const mfx_norm_args* args, void* stream) {
 
 int mfx_softmax(const mfx_norm_args* args, void* stream) {
   return mfx::dispatch<mfx::RowOp::kSoftmax>(args, stream);
+}
+
+int mfx_log_softmax(const mfx_norm_args* args, void* stream) {
+  return mfx::dispatch<mfx::RowOp::kLogSoftmax>(args, stream);
 }
 
 }  // extern "C"

@@ -135,8 +135,9 @@ void inline_calls(Module& m);
 // Fuses attention / normalisation / softmax subgraphs and the reference's
 // custom_call targets into mfx.* nodes; returns the number of rewrites.
 struct RewriteStats {
-  int sdpa = 0, layer_norm = 0, rms_norm = 0, softmax = 0, custom_calls = 0, affine_absorbed = 0;
-  int total() const { return sdpa + layer_norm + rms_norm + softmax + custom_calls; }
+  int sdpa = 0, layer_norm = 0, rms_norm = 0, softmax = 0, log_softmax = 0, sigmoid = 0, custom_calls = 0,
+      affine_absorbed = 0;
+  int total() const { return sdpa + layer_norm + rms_norm + softmax + log_softmax + sigmoid + custom_calls; }
 };
 RewriteStats rewrite(Function& f);
 

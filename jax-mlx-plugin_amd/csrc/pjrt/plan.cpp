@@ -227,7 +227,8 @@ class Planner {
   static void check_supported(const Node& n) {
     static const std::set<std::string> ok = {
         "stablehlo.dot_general", "stablehlo.dot", "stablehlo.reduce", "mfx.sdpa", "mfx.layer_norm",
-        "mfx.rms_norm", "mfx.softmax", "mfx.layer_norm_bwd", "mfx.sdpa_bwd", "stablehlo.concatenate"};
+        "mfx.rms_norm", "mfx.softmax", "mfx.log_softmax", "mfx.layer_norm_bwd", "mfx.sdpa_bwd",
+        "stablehlo.concatenate"};
     if (!ok.count(n.op)) {
       std::string what = n.op;
       if (n.op == "stablehlo.custom_call") what += " @" + n.strs.at("target");
@@ -880,7 +881,7 @@ class Planner {
     check_dense("norm result", out_v, a.rows * a.n);
     if (gamma >= 0) check_dense("norm gamma", gamma, a.n);
     if (beta >= 0) check_dense("norm beta", beta, a.n);
-    int which = n.op == "mfx.layer_norm" ? 0 : n.op == "mfx.rms_norm" ? 1 : 2;
+    int which = n.op == "mfx.layer_norm" ? 0 : n.op == "mfx.rms_norm" ? 1 : n.op == "mfx.softmax" ? 2 : 3;
     auto loc = loc_;
     Plan* plan = &plan_;
     Step s;
@@ -893,8 +894,10 @@ class Planner {
       r.y = plan->ptr((*loc)[out_v], b);
       r.gamma = gamma >= 0 ? plan->ptr((*loc)[gamma], b) : nullptr;
       r.beta = beta >= 0 ? plan->ptr((*loc)[beta], b) : nullptr;
-      int rc = which == 0 ? mfx_layer_norm(&r, b.stream) : which == 1 ? mfx_rms_norm(&r, b.stream)
-                                                                      : mfx_softmax(&r, b.stream);
+      int rc = which == 0   ? mfx_layer_norm(&r, b.stream)
+               : which == 1 ? mfx_rms_norm(&r, b.stream)
+               : which == 2 ? mfx_softmax(&r, b.stream)
+                            : mfx_log_softmax(&r, b.stream);
       if (rc != MFX_OK) err = mfx_last_error();
       return rc;
     };

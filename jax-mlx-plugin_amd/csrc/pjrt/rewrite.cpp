@@ -434,6 +434,23 @@ int rewrite_norms(Ctx& c, RewriteStats& st) {
 
 // ---- softmax -------------------------------------------------------------------
 
+// The row max of a softmax-style chain: reduce_max over the last axis of x
+// [through maximum(-inf, .)], seen through broadcasts.
+bool match_row_max(Ctx& c, int v, int xv, int axis) {
+  int mv = c.strip_all(v);
+  Node* mn = c.def(mv);
+  if (op_is(mn, "stablehlo.maximum")) {
+    double lo;
+    int keep = -1;
+    for (int o = 0; o < 2; ++o)
+      if (c.splat(mn->in[o], lo) && lo < -1e30) keep = mn->in[1 - o];
+    if (keep < 0) return false;
+    mv = keep;
+  }
+  int mx, ma;
+  return match_reduce(c, mv, "stablehlo.maximum", mx, ma) && ma == axis && c.same(mx, xv);
+}
+
 // v == softmax(x) over the last axis; returns x.
 bool match_softmax(Ctx& c, int v, int& x) {
   Node* d = c.def(v);
@@ -449,19 +466,7 @@ bool match_softmax(Ctx& c, int v, int& x) {
   // Denominator: sum of the same exp over the last axis.
   int sx, sa;
   if (!match_reduce(c, d->in[1], "stablehlo.add", sx, sa) || sa != axis || !c.same(sx, e)) return false;
-  // Max: reduce_max(x) [through maximum(-inf, .)].
-  int mv = c.strip_all(sub->in[1]);
-  Node* mn = c.def(mv);
-  if (op_is(mn, "stablehlo.maximum")) {
-    double lo;
-    int keep = -1;
-    for (int o = 0; o < 2; ++o)
-      if (c.splat(mn->in[o], lo) && lo < -1e30) keep = mn->in[1 - o];
-    if (keep < 0) return false;
-    mv = keep;
-  }
-  int mx, ma;
-  if (!match_reduce(c, mv, "stablehlo.maximum", mx, ma) || ma != axis || !c.same(mx, xv)) return false;
+  if (!match_row_max(c, sub->in[1], xv, axis)) return false;
   x = xv;
   return true;
 }
@@ -482,6 +487,86 @@ int rewrite_softmax(Ctx& c, RewriteStats& st) {
     fused.out = n.out;
     n = fused;
     st.softmax++;
+    ++count;
+    c.refresh();
+  }
+  return count;
+}
+
+// v == log_softmax(x) over the last axis, in jax.nn.log_softmax's form
+//   shifted = x - max(x);  v = shifted - log(sum(exp(shifted)))
+// (the computation the reference special-cases for callee @log_softmax,
+// src/jax_mlx_pjrt.cpp:5624-5641); returns x.
+bool match_log_softmax(Ctx& c, int v, int& x) {
+  Node* d = c.def(v);
+  if (!op_is(d, "stablehlo.subtract")) return false;
+  const int shifted = d->in[0];
+  Node* sh = c.def(c.strip_convert(shifted));
+  if (!op_is(sh, "stablehlo.subtract")) return false;
+  const int xv = sh->in[0];
+  const int axis = c.rank(xv) - 1;
+  if (axis < 0) return false;
+  Node* lg = c.def(c.strip_all(d->in[1]));
+  if (!op_is(lg, "stablehlo.log")) return false;
+  int sx, sa;
+  if (!match_reduce(c, lg->in[0], "stablehlo.add", sx, sa) || sa != axis) return false;
+  Node* en = c.def(c.strip_convert(sx));
+  if (!op_is(en, "stablehlo.exponential") || !c.same(en->in[0], shifted)) return false;
+  if (!match_row_max(c, sh->in[1], xv, axis)) return false;
+  x = xv;
+  return true;
+}
+
+int rewrite_log_softmax(Ctx& c, RewriteStats& st) {
+  int count = 0;
+  for (size_t i = 0; i < c.f.nodes.size(); ++i) {
+    Node& n = c.f.nodes[i];
+    if (n.dead || n.op != "stablehlo.subtract" || n.out.size() != 1) continue;
+    int x;
+    if (!match_log_softmax(c, n.out[0], x)) continue;
+    if (c.ty(x) != c.ty(n.out[0])) continue;
+    const DType dt = c.ty(x).dtype;
+    if (dt != DType::kF32 && dt != DType::kBF16) continue;
+    Node fused;
+    fused.op = "mfx.log_softmax";
+    fused.in = {x};
+    fused.out = n.out;
+    n = fused;
+    st.log_softmax++;
+    ++count;
+    c.refresh();
+  }
+  return count;
+}
+
+// 1 / (1 + exp(-x)) -> logistic(x), the reference's sigmoid pattern
+// (src/jax_mlx_pjrt.cpp:2046-2164: divide(1, add(1, exp(negate(x))))).  The
+// result is one elementwise instruction instead of four; intermediates used
+// elsewhere stay computed (the replaced divide is the only node rewritten).
+int rewrite_sigmoid(Ctx& c, RewriteStats& st) {
+  int count = 0;
+  for (size_t i = 0; i < c.f.nodes.size(); ++i) {
+    Node& n = c.f.nodes[i];
+    if (n.dead || n.op != "stablehlo.divide" || n.out.size() != 1) continue;
+    double one;
+    if (!c.splat(n.in[0], one) || one != 1.0) continue;
+    Node* ad = c.def(n.in[1]);
+    if (!op_is(ad, "stablehlo.add")) continue;
+    int e = -1;
+    for (int o = 0; o < 2; ++o)
+      if (c.splat(ad->in[o], one) && one == 1.0) e = ad->in[1 - o];
+    Node* en = e >= 0 ? c.def(e) : nullptr;
+    if (!op_is(en, "stablehlo.exponential")) continue;
+    Node* ng = c.def(en->in[0]);
+    if (!op_is(ng, "stablehlo.negate")) continue;
+    const int x = ng->in[0];
+    if (c.ty(x) != c.ty(n.out[0])) continue;
+    Node fused;
+    fused.op = "stablehlo.logistic";
+    fused.in = {x};
+    fused.out = n.out;
+    n = fused;
+    st.sigmoid++;
     ++count;
     c.refresh();
   }
@@ -1351,6 +1436,8 @@ RewriteStats rewrite(Function& f) {
   Ctx c3(f);
   fold_rms_into_sdpa(c3);
   rewrite_softmax(c3, st);
+  rewrite_log_softmax(c3, st);
+  rewrite_sigmoid(c3, st);
   compact(f);
   return st;
 }
@@ -1408,6 +1495,7 @@ std::string to_json(const Function& f, const RewriteStats* stats) {
   if (stats)
     o << ", \"rewrites\": {\"sdpa\": " << stats->sdpa << ", \"layer_norm\": " << stats->layer_norm
       << ", \"rms_norm\": " << stats->rms_norm << ", \"softmax\": " << stats->softmax
+      << ", \"log_softmax\": " << stats->log_softmax << ", \"sigmoid\": " << stats->sigmoid
       << ", \"custom_calls\": " << stats->custom_calls << ", \"affine_absorbed\": " << stats->affine_absorbed
       << "}";
   o << "}";

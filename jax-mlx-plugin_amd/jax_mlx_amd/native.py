@@ -147,7 +147,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.mfx_last_error.restype = ctypes.c_char_p
     lib.mfx_version.restype = ctypes.c_int
     lib.mfx_device_count.restype = ctypes.c_int
-    for name in ("mfx_layer_norm", "mfx_rms_norm", "mfx_softmax"):
+    for name in ("mfx_layer_norm", "mfx_rms_norm", "mfx_softmax", "mfx_log_softmax"):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.POINTER(NormArgs), ctypes.c_void_p]
         fn.restype = ctypes.c_int
@@ -259,6 +259,11 @@ def rms_norm(x, weight=None, eps: float = 1e-5, out=None):
 def softmax(x, out=None):
     """Softmax over the last axis (mfx_softmax)."""
     return _norm_call("mfx_softmax", x, None, None, 0.0, out)
+
+
+def log_softmax(x, out=None):
+    """Log-softmax over the last axis (mfx_log_softmax)."""
+    return _norm_call("mfx_log_softmax", x, None, None, 0.0, out)
 
 
 def layer_norm_bwd(x, dy, gamma=None, eps: float = 1e-5, *, param_grads=True, param_dtype=None,

@@ -15,6 +15,7 @@
  *   oracle_rms_norm     src/jax_mlx_pjrt.cpp:2166-2169 (x*rsqrt(mean(x^2)+eps),
  *                       optional weight), executed at :4422-4429.
  *   oracle_softmax      src/jax_mlx_pjrt.cpp:1857-2044 (exp(x-max)/sum).
+ *   oracle_log_softmax  src/jax_mlx_pjrt.cpp:5624-5641 ((x-max) - log(sum(exp(x-max)))).
  *   oracle_sdpa         src/jax_mlx/sdpa.py:19-31 and src/jax_mlx_pjrt.cpp:
  *                       2491-2495 (softmax(scale*QK^T + M) V) in BHTD layout;
  *                       M is 0, causal (key j allowed iff j <= query i, top-left
@@ -81,6 +82,22 @@ ORACLE_API void oracle_rms_norm(const double* x, const double* weight,
       if (weight) v *= weight[i];
       yr[i] = v;
     }
+  }
+}
+
+/* Row log-softmax: shifted = x - max(x), y = shifted - log(sum(exp(shifted))).
+ * An all -inf row yields NaN, as the shifted difference does. */
+ORACLE_API void oracle_log_softmax(const double* x, int64_t rows, int64_t n,
+                                   double* y) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const double* xr = x + r * n;
+    double* yr = y + r * n;
+    double m = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) m = xr[i] > m ? xr[i] : m;
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) s += exp(xr[i] - m);
+    const double ls = log(s);
+    for (int64_t i = 0; i < n; ++i) yr[i] = (xr[i] - m) - ls;
   }
 }
 

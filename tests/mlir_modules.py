@@ -256,6 +256,50 @@ def softmax_module(shape=(6, 64), dt="f32"):
     return module("jit_softmax", [f.text([y], [ty(shape, dt)]), softmax_fn(shape, dt)])
 
 
+def log_softmax_fn(shape, dt="f32", name="log_softmax"):
+    """jax.nn.log_softmax(x, axis=-1) as the private function JAX emits:
+    x_max = max(x, initial=-inf, keepdims); shifted = x - x_max;
+    shifted - log(sum(exp(shifted), keepdims))."""
+    f = Fn(name, [(shape, dt)], public=False)
+    x = f.arg(0)
+    r = len(shape) - 1
+    m, mshape = f.reduce(x, shape, [r], "maximum", dt)
+    m = f.binary("maximum", f.splat(-math.inf, mshape, dt), m, mshape, dt)
+    kshape = list(mshape) + [1]
+    m = f.bcast(m, mshape, list(range(r)), kshape, dt)
+    shifted = f.binary("subtract", x, f.bcast(m, kshape, list(range(r + 1)), shape, dt), shape, dt)
+    e = f.unary("exponential", shifted, shape, dt)
+    s, sshape = f.reduce(e, shape, [r], "add", dt)
+    s = f.bcast(s, sshape, list(range(r)), kshape, dt)
+    lg = f.unary("log", s, kshape, dt)
+    out = f.binary("subtract", shifted, f.bcast(lg, kshape, list(range(r + 1)), shape, dt), shape, dt)
+    return f.text([out], [ty(shape, dt)])
+
+
+def log_softmax_module(shape=(6, 64), dt="f32"):
+    shape = list(shape)
+    f = Fn("main", [(shape, dt)])
+    y = f.call("log_softmax", [f.arg(0)], [ty(shape, dt)], ty(shape, dt))
+    return module("jit_log_softmax", [f.text([y], [ty(shape, dt)]), log_softmax_fn(shape, dt)])
+
+
+def sigmoid_silu_module(shape=(16, 256), dt="f32"):
+    """Two results: the divide form of the sigmoid the reference matches
+    (1 / (1 + exp(-x)), src/jax_mlx_pjrt.cpp:2046-2164) and jax.nn.silu as a
+    private @silu function (x * logistic(x))."""
+    shape = list(shape)
+    f = Fn("main", [(shape, dt)])
+    x = f.arg(0)
+    den = f.binary("add", f.splat(1.0, shape, dt), f.unary("exponential", f.unary("negate", x, shape, dt), shape, dt),
+                   shape, dt)
+    sig = f.binary("divide", f.splat(1.0, shape, dt), den, shape, dt)
+    si = f.call("silu", [x], [ty(shape, dt)], ty(shape, dt))
+    g = Fn("silu", [(shape, dt)], public=False)
+    y = g.binary("multiply", g.arg(0), g.unary("logistic", g.arg(0), shape, dt), shape, dt)
+    return module("jit_sigmoid_silu", [f.text([sig, si], [ty(shape, dt), ty(shape, dt)]),
+                                       g.text([y], [ty(shape, dt)])])
+
+
 # ---------------------------------------------------------------- attention
 
 def _causal_pred(f, T, S):

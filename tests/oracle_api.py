@@ -31,6 +31,7 @@ def _load():
     lib.oracle_layer_norm.argtypes = [_dp, _dp, _dp, _i64, _i64, ctypes.c_double, _dp]
     lib.oracle_rms_norm.argtypes = [_dp, _dp, _i64, _i64, ctypes.c_double, _dp]
     lib.oracle_softmax.argtypes = [_dp, _i64, _i64, _dp]
+    lib.oracle_log_softmax.argtypes = [_dp, _i64, _i64, _dp]
     lib.oracle_sdpa.argtypes = [_dp, _dp, _dp, _dp, ctypes.POINTER(_i64)] + [_i64] * 7 + [
         ctypes.c_double, ctypes.c_int, _dp]
     lib.oracle_sdpa.restype = ctypes.c_int
@@ -73,6 +74,14 @@ def softmax(x):
     y = np.empty_like(x)
     n = x.shape[-1]
     _load().oracle_softmax(xp, x.size // n, n, y.ctypes.data_as(_dp))
+    return y
+
+
+def log_softmax(x):
+    x, xp = _c(x)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    _load().oracle_log_softmax(xp, x.size // n, n, y.ctypes.data_as(_dp))
     return y
 
 

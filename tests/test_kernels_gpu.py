@@ -183,6 +183,26 @@ def test_softmax_f32(cuda, nat, oracle, shape):
     np.testing.assert_allclose(host(nat.softmax(cuda.ones(1, 5, device="cuda"))), 0.2, atol=1e-7)
 
 
+@pytest.mark.parametrize("shape,dtype", [((6, 64), "f32"), ((4, 1000), "f32"), ((3, 2048), "f32"), ((2, 12), "f32"),
+                                         ((5, 6000), "f32"), ((33, 77), "f32"), ((8, 512), "bf16"), ((3, 40), "bf16")])
+def test_log_softmax(cuda, nat, oracle, shape, dtype):
+    """mfx_log_softmax against the fp64 oracle: f32 max-abs <= 1e-5 *
+    max(1, |ref|) (log-probabilities reach -40 here); bf16 the relative bar."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(shape).astype(np.float32) * 4
+    x[0, 1] = -np.inf
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    xd = dev(cuda, x, td)
+    y = host(nat.log_softmax(xd))
+    ref = oracle.log_softmax(host(xd))
+    assert np.isneginf(y[0, 1]) and np.isneginf(ref[0, 1])
+    ok = np.isfinite(ref)
+    if dtype == "f32":
+        assert np.abs(y[ok] - ref[ok]).max() <= F32_NORM_TOL * max(1.0, np.abs(ref[ok]).max())
+    else:
+        assert rel_inf(y[ok], ref[ok]) <= BF16_REL_TOL
+
+
 # ---------------------------------------------------------------- SDPA
 
 def make_qkv(torch, seed, qshape, kshape, dtype, vshape=None):

@@ -65,6 +65,24 @@ def test_rms_norm_closed_forms(oracle):
     np.testing.assert_allclose(oracle.rms_norm(x, None, 0.0), x / np.sqrt(14.0 / 3.0), atol=TOL)
 
 
+def test_log_softmax_against_scipy_and_invariants(oracle):
+    """log-softmax pins: scipy.special.log_softmax (the routine the reference's
+    own tests compare against, tests/test_exhaustive.py:688-689), rows whose
+    logsumexp is 0, shift invariance, and the uniform row log(1/n)."""
+    import scipy.special
+
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((7, 33)) * 5
+    y = oracle.log_softmax(x)
+    np.testing.assert_allclose(y, scipy.special.log_softmax(x, axis=-1), atol=1e-12)
+    np.testing.assert_allclose(scipy.special.logsumexp(y, axis=-1), 0.0, atol=1e-12)
+    np.testing.assert_allclose(oracle.log_softmax(x + 1e3), y, atol=1e-9)
+    np.testing.assert_allclose(oracle.log_softmax(np.ones((2, 5))), np.log(0.2), atol=1e-15)
+    # exp(log_softmax) is the softmax oracle
+    np.testing.assert_allclose(np.exp(y), oracle.softmax(x), atol=1e-12)
+    assert np.isnan(oracle.log_softmax(np.full((1, 4), -np.inf))).all()
+
+
 def test_softmax_matches_golden_and_reference_kat(oracle, golden):
     np.testing.assert_allclose(oracle.softmax(golden["softmax_x"]), golden["softmax_y"], atol=TOL)
     # Reference KAT: nn.softmax(ones(5)) == 0.2 (tests/test_exhaustive.py:749).

@@ -203,6 +203,23 @@ def test_softmax_through_func_call(api):
     assert [n["op"] for n in fused(d)] == ["mfx.softmax"] and steps(d) == ["softmax"]
 
 
+def test_log_softmax_through_func_call(api):
+    d = api.inspect(M.log_softmax_module((6, 64)))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.log_softmax"
+    assert steps(d) == ["log_softmax"]
+    assert d["graph"]["rewrites"]["log_softmax"] == 1
+
+
+def test_sigmoid_divide_form_and_silu(api):
+    d = api.inspect(M.sigmoid_silu_module((16, 256)))
+    assert d["graph"]["rewrites"]["sigmoid"] == 1
+    ops = [n["op"] for n in d["graph"]["nodes"]]
+    assert "stablehlo.divide" not in ops and "stablehlo.exponential" not in ops
+    assert ops.count("stablehlo.logistic") == 2  # the rewritten divide and silu's own
+    assert steps(d) == ["elementwise", "elementwise"]
+
+
 def test_softmax_on_leading_axis_is_not_fused(api):
     shape = [64, 6]
     f = M.Fn("main", [(shape, "f32")])

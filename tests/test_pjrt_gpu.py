@@ -255,6 +255,40 @@ def test_gqa_decode_with_q_rms(client, oracle, S):
     assert rel_inf(o, ref) <= BF16_REL_TOL
 
 
+@pytest.mark.parametrize("shape,dt", [((6, 64), "f32"), ((4, 1000), "f32"), ((16, 2048), "bf16")])
+def test_log_softmax_fused(client, oracle, shape, dt):
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal(shape).astype(np.float32) * 3
+    if dt == "bf16":
+        x = bf16_round(x)
+    (y,) = run(client, M.log_softmax_module(shape, dt), [x], [dt])
+    ref = oracle.log_softmax(x)
+    if dt == "f32":
+        assert np.abs(y - ref).max() <= F32_NORM_TOL * max(1.0, np.abs(ref).max())
+    else:
+        assert rel_inf(y, ref) <= BF16_REL_TOL
+
+
+@pytest.mark.parametrize("shape,dt", [((16, 256), "f32"), ((7, 33), "f32"), ((8, 128), "bf16")])
+def test_sigmoid_and_silu(client, shape, dt):
+    """The sigmoid divide form (rewritten to one logistic instruction) and
+    silu through func.call, against numpy fp64: f32 max-abs <= 1e-6 (values
+    in [0, 1] and |x|-scaled), bf16 the relative bar."""
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal(shape).astype(np.float32) * 4
+    if dt == "bf16":
+        x = bf16_round(x)
+    sig, si = run(client, M.sigmoid_silu_module(shape, dt), [x], [dt])
+    xs = x.astype(np.float64)
+    ref_sig = 1.0 / (1.0 + np.exp(-xs))
+    ref_si = xs * ref_sig
+    if dt == "f32":
+        assert np.abs(sig - ref_sig).max() <= 1e-6
+        assert np.abs(si - ref_si).max() <= 1e-6 * max(1.0, np.abs(ref_si).max())
+    else:
+        assert rel_inf(sig, ref_sig) <= BF16_REL_TOL and rel_inf(si, ref_si) <= BF16_REL_TOL
+
+
 # ------------------------------------------------------ generic elementwise
 
 @pytest.mark.parametrize("R,C,dt", [(64, 256, "f32"), (33, 77, "f32"), (8, 1024, "bf16"), (5, 12, "bf16"),
