@@ -14,6 +14,7 @@ struct Plan {
   Kind kind = Kind::kGeneric;
   size_t partial_bytes = 0;  // split-KV partials
   size_t qnorm_bytes = 0;    // normalised q for kernels without fused RMSNorm
+  int decode_waves = 0;      // MFMA decode: wavefronts of the main kernel
 };
 
 int make_plan(const mfx_sdpa_args* a, Plan& out) {
@@ -64,23 +65,20 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
   p.split_len = p.Tk;
 
   if (p.Tq <= 4 && decode_mfma_supports(p)) {
-    // W wavefronts per (batch, kv head), wavefront j owning tiles j, j+W, ...:
-    // at most 1024 wavefronts in all (four 32 KB-LDS workgroups per CU, the
-    // whole grid resident at once, so no second round forms a tail), at
-    // least two tiles each, at most the tile bitmap's width each.
+    // W wavefronts split the listed (visible) tiles of all kv heads into
+    // equal ranges: as many as stay resident at once (three 48 KB-LDS
+    // workgroups per CU at d = 128, six at d = 64, on 256 CUs), at most one
+    // per tile.
     out.kind = Kind::kDecodeMfma;
-    const int pairs = p.B * p.Hkv;
-    const int tiles = (p.Tk + decode_mfma_tile() - 1) / decode_mfma_tile();
-    int w = 1024 / pairs;
-    if (w > (tiles + 1) / 2) w = (tiles + 1) / 2;
-    const int wmin = (tiles + decode_mfma_max_tiles() - 1) / decode_mfma_max_tiles();
-    if (w < wmin) w = wmin;
-    if (w < 1) w = 1;
-    const int splits = w;
-    p.num_splits = splits;
-    p.split_len = 0;
-    if (splits > 1)
-      out.partial_bytes = (size_t)splits * p.B * p.Hq * p.Tq * (p.Dv + 2) * sizeof(float);
+    const int64_t tiles = (int64_t)p.B * p.Hkv * ((p.Tk + decode_mfma_tile() - 1) / decode_mfma_tile());
+    const int64_t resident = p.D == 128 ? 768 : 1536;
+    out.decode_waves = (int)(tiles < resident ? tiles : resident);
+    // Vector mask loads: contiguous keys, every row start 4-element aligned,
+    // Tk a whole number of runs of four keys.
+    const int msz = p.mask_dtype == MFX_F32 ? 4 : 2;
+    p.mask_vec4 = p.mask && p.ms[3] == 1 && p.Tk % 4 == 0 && (uintptr_t)p.mask % (4 * msz) == 0 &&
+                  p.ms[0] % 4 == 0 && p.ms[1] % 4 == 0 && p.ms[2] % 4 == 0;
+    out.partial_bytes = decode_mfma_workspace(p, out.decode_waves);
     return MFX_OK;
   }
   if (p.Tq <= 4 && decode_supports(p)) {
@@ -157,7 +155,8 @@ int mfx_sdpa_fwd(const mfx_sdpa_args* args, void* stream) {
     }
   }
   SdpaParams& p = pl.p;
-  if (pl.partial_bytes) p.partial = reinterpret_cast<float*>(ws);
+  if (pl.kind == Kind::kDecodeMfma) decode_mfma_bind(p, pl.decode_waves, ws);
+  else if (pl.partial_bytes) p.partial = reinterpret_cast<float*>(ws);
   if (pl.qnorm_bytes) {
     // Kernels without a fused q RMSNorm read a normalised copy of q.
     void* qn = ws + align256(pl.partial_bytes);

@@ -24,6 +24,15 @@ struct SdpaParams {
   float q_rms_eps;   // < 0: no RMSNorm on q
   int num_splits;    // split-KV decode only: partials per row
   int split_len;     // keys per split (VALU decode; the MFMA decode interleaves tiles)
+  // MFMA decode work lists (workspace): per (batch, kv head) the indices of
+  // the key tiles with a visible key, tile_list[bhk * tiles_cap + i], and
+  // their number tile_count[bhk].
+  int* tile_list;
+  int* tile_count;
+  int tiles_cap;
+  // Mask rows are contiguous along keys and 4-element aligned (so a lane's
+  // four consecutive keys are one vector load).
+  int mask_vec4;
   // Optional: row log-sum-exp of the scaled scores in log2 units,
   // lse[(b * Hq + h) * Tq + i] = log2(sum_j exp2(s_ij)), written by the
   // flash and generic kernels when non-null (the backward pass reads it).
@@ -71,8 +80,24 @@ bool flash_bf16_supports(const SdpaParams& p);
 bool flash_f32_supports(const SdpaParams& p);
 bool decode_supports(const SdpaParams& p);
 bool decode_mfma_supports(const SdpaParams& p);
-int decode_mfma_tile();       // keys per tile of the MFMA decode
-int decode_mfma_max_tiles();  // tiles one of its wavefronts can own
+int decode_mfma_tile();  // keys per tile of the MFMA decode
+// Workspace bytes of the MFMA decode with W wavefronts: tile lists, counts and
+// the (W + B*Hkv) * R partial rows.
+size_t decode_mfma_workspace(const SdpaParams& p, int W);
+// Lays the MFMA decode's work lists and partials out in `ws` (which holds
+// decode_mfma_workspace bytes) and sets p.num_splits = W.
+void decode_mfma_bind(SdpaParams& p, int W, void* ws);
+
+// Mask element type as a compile-time code: 1 f32, 2 bf16, 3 f16 (0: no
+// mask).  Typed loads keep the conversion out of a runtime branch, so the
+// compiler need not wait for the load inside it.
+inline int mask_code(int dt) { return dt == MFX_F32 ? 1 : dt == MFX_BF16 ? 2 : 3; }
+template <int MT>
+__device__ __forceinline__ float load_mask_t(const void* m, int64_t off) {
+  if constexpr (MT == 1) return static_cast<const float*>(m)[off];
+  else if constexpr (MT == 2) return static_cast<float>(static_cast<const bf16*>(m)[off]);
+  else return static_cast<float>(static_cast<const _Float16*>(m)[off]);
+}
 
 // Loads one additive-mask element as fp32.
 __device__ __forceinline__ float load_mask(const void* m, int dt, int64_t off) {

@@ -3,10 +3,7 @@
 //
 // The R = (Hq/Hkv) * Tq query rows that share one kv head (R <= 32) are the
 // columns of one 32-wide MFMA operand, so every K/V row is read from HBM once
-// for all of them.  The grid is (B*Hkv, W): W wavefronts (one per workgroup)
-// share a kv head and wavefront j takes the 32-key tiles j, j+W, j+2W, ...,
-// so every wavefront gets an equal share of a valid prefix (a length-masked
-// cache) and the partial results of the W wavefronts merge at the end:
+// for all of them:
 //   S^T = K Q^T   A = K tile rows (LDS), B = the R query rows (registers,
 //                 zero-padded to 32 columns): v_mfma_f32_32x32x16_bf16.
 //   O^T = V^T P^T A = transposing LDS reads of the V tile, B = P straight
@@ -15,12 +12,20 @@
 // The padding wastes MFMA work that costs a few microseconds against the
 // tens of microseconds the K/V bytes take: the kernel is HBM-bound.
 //
-// K/V tiles stream through two swizzled LDS stages by asynchronous LDS-DMA
-// loads; while one tile is computed, the next valid tile is in flight.  A
-// prepass marks the tiles that hold at least one visible key (additive mask
-// not -inf for some row, key < Tk, causal limit), and only those are
-// loaded, so a padded KV cache costs the bytes of its valid prefix.  The W
-// partials (m, l, O) of a row merge in the split-KV combine kernel.
+// Work is balanced over the valid bytes, not over Tk.  A first kernel lists,
+// per (batch, kv head), the 32-key tiles holding at least one visible key
+// (additive mask not -inf for some row, key < Tk, causal limit).  The W
+// wavefronts of the main kernel then split the concatenation of all lists
+// into W equal contiguous ranges, so a batch with a long valid cache gets
+// proportionally more wavefronts and every wavefront streams the same number
+// of tiles.  A range may cross (batch, kv head) boundaries: each segment of
+// it writes one partial (m, l, O) per row into slot (wavefront + bhk), which
+// is unique because ranges are ordered, and the combine kernel merges the
+// slots of the wavefronts whose range meets that bhk.
+//
+// K/V tiles stream through three swizzled LDS stages by asynchronous LDS-DMA
+// loads; while one tile is computed, the next two are in flight (the kernel
+// is bound by bytes in flight per CU, which the 160 KB of LDS caps).
 //
 // Optional fused RMSNorm of the query rows (reference chain rms_norm -> sdpa
 // of GQA decode): q is normalised in fp32 and rounded to bf16 before it is
@@ -37,10 +42,9 @@ using tiles::lds_s16x4_t;
 using tiles::s16x4;
 using tiles::tile_swz;
 
-constexpr int kDN = 32;  // keys per tile: 32 KB of LDS per workgroup, five per CU
+constexpr int kDN = 32;  // keys per tile: three stages = 48 KB of LDS per workgroup, three per CU
 constexpr int kMT = kDN / 32;
 constexpr int kKS = kDN / 16;
-constexpr int kMaxTiles = 64;  // per wavefront: width of the valid-tile bitmap
 
 // s_waitcnt vmcnt(N) with the other counters left alone (N < 64).
 template <int N>
@@ -49,129 +53,139 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-template <int D, bool MASK, bool CAUSAL>
+// Lists, per (batch, kv head), the tiles holding a key some row can see.
+// One workgroup per bhk.  Phase 1 reads the mask coalesced: thread t checks
+// keys j*256 + t (j = 0, 1, ...), so the 32 keys of a tile sit in 32
+// consecutive lanes and one ballot per load gives two tiles' flags, which go
+// to LDS.  Phase 2 compacts the flagged tiles in tile order (one thread per
+// tile, a ballot per wavefront and a prefix over the four wavefronts).  The
+// mask is read per row of the group only when it varies over heads or query
+// positions.
+template <int MT, bool CAUSAL>
+__global__ __launch_bounds__(256) void decode_tiles_kernel(SdpaParams p) {
+  constexpr bool MASK = MT != 0;
+  constexpr int kPass = 256;  // tiles flagged per pass (256 * 32 keys)
+  __shared__ int flag[kPass];
+  __shared__ int wave_n[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int bhk = blockIdx.x;
+  const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
+  const int Tq = p.Tq, R = p.group * Tq, Tk = p.Tk;
+  const int kend = CAUSAL ? min(Tk, Tq) : Tk;  // keys past this are never visible
+  const int ntile = (Tk + kDN - 1) / kDN;
+  int* list = p.tile_list + (int64_t)bhk * p.tiles_cap;
+  const bool bcast = !MASK || ((p.ms[1] == 0 || p.group == 1) && (p.ms[2] == 0 || Tq == 1));
+  const int rows = bcast ? 1 : R;
+  int n = 0;  // tiles listed so far (uniform)
+  for (int t0 = 0; t0 < ntile; t0 += kPass) {
+    // Phase 1: flags of tiles t0 .. t0 + kPass - 1.
+    // All kB loads of a thread's keys are in flight together.
+    constexpr int kB = kPass * kDN / 256;
+    bool ok[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) ok[u] = t0 * kDN + u * 256 + tid < kend;
+    if constexpr (MASK) {
+      bool any[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) any[u] = false;
+      for (int r = 0; r < rows; ++r) {
+        const int h2 = hk * p.group + r / Tq, t2 = r % Tq;
+        const int64_t mrow = b * p.ms[0] + (bcast ? 0 : h2 * p.ms[1] + t2 * p.ms[2]);
+        float mvv[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const int key = min(t0 * kDN + u * 256 + tid, Tk - 1);
+          mvv[u] = load_mask_t<MT>(p.mask, mrow + (int64_t)key * p.ms[3]);
+        }
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const int key = t0 * kDN + u * 256 + tid;
+          any[u] = any[u] | ((mvv[u] != -INFINITY) & (bcast | !CAUSAL | (key <= t2)));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kB; ++u) ok[u] = ok[u] & any[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const uint64_t bal = __ballot(ok[u]);
+      // lanes 0-31 / 32-63 of wavefront wv hold tile u*8 + wv*2 + 0 / 1
+      if (lane == 0) {
+        flag[u * 8 + wv * 2] = (bal & 0xffffffffull) != 0;
+        flag[u * 8 + wv * 2 + 1] = (bal >> 32) != 0;
+      }
+    }
+    __syncthreads();
+    // Phase 2: compaction in tile order.
+    const bool listed = t0 + tid < ntile && flag[tid];
+    const uint64_t bal = __ballot(listed);
+    if (lane == 0) wave_n[wv] = __popcll(bal);
+    __syncthreads();
+    int before = n;
+    for (int i = 0; i < wv; ++i) before += wave_n[i];
+    const int total = wave_n[0] + wave_n[1] + wave_n[2] + wave_n[3];
+    if (listed) list[before + __popcll(bal & ((1ull << lane) - 1))] = t0 + tid;
+    n += total;
+    __syncthreads();
+  }
+  if (tid == 0) p.tile_count[bhk] = n;
+}
+
+// First element of wavefront w's range of the concatenated tile lists.
+__device__ __forceinline__ int64_t range_start(int w, int64_t T, int W) { return (int64_t)w * T / W; }
+
+template <int D, int MT, bool CAUSAL>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
+  constexpr bool MASK = MT != 0;
   using Loader = tiles::TileLoader<D, kDN, 1>;
   __shared__ __attribute__((aligned(16))) bf16 k0[kDN * D];
   __shared__ __attribute__((aligned(16))) bf16 v0[kDN * D];
   __shared__ __attribute__((aligned(16))) bf16 k1[kDN * D];
   __shared__ __attribute__((aligned(16))) bf16 v1[kDN * D];
+  __shared__ __attribute__((aligned(16))) bf16 k2[kDN * D];
+  __shared__ __attribute__((aligned(16))) bf16 v2[kDN * D];
 
   const int lane = threadIdx.x;
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.y, bhk = blockIdx.x;  // split = this wavefront's tile phase j
-  const int W = p.num_splits;
-  const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
+  const int w = blockIdx.x, W = gridDim.x;
+  const int BHk = p.B * p.Hkv;
   const int Tq = p.Tq, R = p.group * Tq, Tk = p.Tk;
-
-  // This lane's query column (rows past R are zero and never stored).
-  const bool qvalid = col < R;
-  const int rr = qvalid ? col : 0;
-  const int hq = hk * p.group + rr / Tq, tq = rr % Tq;
-
-  bf16x8 qf[D / 16];
-  {
-    const bf16* qrow = static_cast<const bf16*>(p.q) + b * p.qs[0] + hq * p.qs[1] + tq * p.qs[2] + half * 8;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + kk * 16);
-      if (!qvalid) raw = u32x4{0u, 0u, 0u, 0u};
-      qf[kk] = __builtin_bit_cast(bf16x8, raw);
-    }
-  }
-  if (p.q_rms_eps >= 0.f) {
-    // Lane holds d = kk*16 + half*8 + e; lanes col and col+32 hold one row.
-    float ss = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = static_cast<float>(qf[kk][e]);
-        ss += x * x;
-      }
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-    ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
-    const bf16* w = static_cast<const bf16*>(p.q_rms_weight);
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float t = static_cast<float>(qf[kk][e]) * inv;
-        if (w) t *= static_cast<float>(w[kk * 16 + half * 8 + e]);
-        qf[kk][e] = static_cast<bf16>(t);
-      }
-  }
   const float sl2 = p.scale_log2;  // > 0 (checked on the host)
 
-  // This wavefront's tiles: global tile split + W*i, i = 0 .. ntile-1.
-  const int tiles_total = (Tk + kDN - 1) / kDN;
-  const int ntile = split < tiles_total ? (tiles_total - split + W - 1) / W : 0;  // <= kMaxTiles (host)
-  int64_t m_base = 0;
-  if constexpr (MASK) m_base = b * p.ms[0] + hq * p.ms[1] + tq * p.ms[2];
-
-  // Prepass: bit i set when local tile i holds a key some row can see.  Lane
-  // l checks key (l % 32) of local tile 2c + l/32; the loads of all chunks
-  // are issued eight at a time, so the whole prepass costs one or two round
-  // trips.  A mask that does not vary over heads and query positions is
-  // checked once per key, otherwise once per (row, key).
-  uint64_t vbits = 0;
-  {
-    const bool bcast = !MASK || ((p.ms[1] == 0 || p.group == 1) && (p.ms[2] == 0 || Tq == 1));
-    const int nchunk = (ntile + 1) / 2;
-    for (int c0 = 0; c0 < nchunk; c0 += 8) {
-      bool ok[8];
-      int keyj[8];
+  // Total listed tiles and this wavefront's range [s, e) of them: the
+  // counts are read 64 per vector load and summed across lanes (a scalar
+  // load per count would put ~BHk memory round trips before the first DMA).
+  int64_t T = 0;
+  for (int i0 = 0; i0 < BHk; i0 += 64) {
+    int c = i0 + lane < BHk ? p.tile_count[i0 + lane] : 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = 2 * (c0 + j) + (lane >> 5);
-        const int key = (split + W * i) * kDN + (lane & 31);
-        keyj[j] = min(key, Tk - 1);
-        ok[j] = i < ntile && key < Tk;
-        if (CAUSAL) ok[j] = ok[j] && key <= Tq - 1;
-      }
-      if constexpr (MASK) {
-        if (bcast) {
-          float mvv[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) mvv[j] = load_mask(p.mask, p.mask_dtype, b * p.ms[0] + (int64_t)keyj[j] * p.ms[3]);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) ok[j] = ok[j] && mvv[j] != -INFINITY;
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            bool any = false;
-            for (int r = 0; r < R; ++r) {
-              const int h2 = hk * p.group + r / Tq, t2 = r % Tq;
-              const float mvv = load_mask(p.mask, p.mask_dtype,
-                                          b * p.ms[0] + h2 * p.ms[1] + t2 * p.ms[2] + (int64_t)keyj[j] * p.ms[3]);
-              any |= mvv != -INFINITY && (!CAUSAL || keyj[j] <= t2);
-            }
-            ok[j] = ok[j] && any;
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint64_t bal = __ballot(ok[j]);
-        const int i = 2 * (c0 + j);
-        if ((bal & 0xffffffffull) && i < kMaxTiles) vbits |= 1ull << i;
-        if ((bal >> 32) && i + 1 < kMaxTiles) vbits |= 1ull << (i + 1);
-      }
-    }
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    T += __builtin_amdgcn_readfirstlane(c);
   }
-
-  const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
-  const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
-  const Loader kload(kp, p.ks[2], Tk, 0, lane), vload(vp, p.vs[2], Tk, 0, lane);
-  auto gtile = [&](int i) { return split + W * i; };
-
-  f32x16 o[D / 32];
+  int64_t s = range_start(w, T, W);
+  const int64_t e = range_start(w + 1, T, W);
+  if (s >= e) return;
+  // The bhk holding element s and the first element of its list: inclusive
+  // prefix sums across lanes, then the first lane whose prefix passes s.
+  int bhk = 0;
+  int64_t P = 0;
+  for (int i0 = 0; i0 < BHk; i0 += 64) {
+    const int c = i0 + lane < BHk ? p.tile_count[i0 + lane] : 0;
+    int incl = c;
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-  float b_run = -INFINITY, l_run = 0.f;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    const uint64_t hit = __ballot(P + incl > s);
+    if (hit) {
+      const int l0 = __builtin_ctzll(hit);
+      bhk = i0 + l0;
+      P += __builtin_amdgcn_readlane(incl - c, l0);
+      break;
+    }
+    P += __builtin_amdgcn_readlane(incl, 63);
+  }
 
   // Per-lane byte offsets of the operand reads within a tile (the same
   // patterns as the prefill kernel).
@@ -192,189 +206,438 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       v_addr[dt][1] = (uint32_t)(((v_row + 8) * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw8) * 8) * 2);
     }
   }
+  const bool qvalid = col < R;
+  const int rr = qvalid ? col : 0;
 
-  // Mask values of tile tn in the S^T lane layout (keys past Tk clamped:
-  // they are masked by the key < Tk test).
-  float mv_next[kMT][16];
-  auto load_tile_mask = [&](int tn) __attribute__((always_inline)) {
-    const int kb = gtile(tn) * kDN;
+  // One segment per (batch, kv head) the range meets.  At most BHk
+  // iterations; every iteration advances s by at least one tile.
+  for (int guard = 0; guard < BHk && s < e; ++guard) {
+    const int cnt = p.tile_count[bhk];
+    const int64_t seg_end = e < P + cnt ? e : P + cnt;
+    const int* lst = p.tile_list + (int64_t)bhk * p.tiles_cap + (s - P);
+    const int ntl = (int)(seg_end - s);
+    // The segment's tile indices live in VGPRs, entries [wb, wb + 64),
+    // [wb + 64, wb + 128) and [wb + 128, wb + 192), read with readlane: no
+    // memory round trip sits between a tile and the DMA of the tile two
+    // places later.  When tile i leaves the first register the window moves
+    // by 64, and the new third register is loaded 64 tiles before any entry
+    // of it is read (its load only lengthens the vmcnt waits below).
+    auto list_at = [&](int j) { return j < ntl ? lst[j] : 0; };
+    int w0 = list_at(lane), w1 = list_at(64 + lane), w2 = list_at(128 + lane);
+    int wb = 0;
+    auto tile_at = [&](int i) __attribute__((always_inline)) {
+      const int r = i - wb;
+      return r < 64 ? __builtin_amdgcn_readlane(w0, r) : __builtin_amdgcn_readlane(w1, r - 64);
+    };
+    const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
+    const int hq = hk * p.group + rr / Tq, tq = rr % Tq;
+
+    // This lane's query column (rows past R are zero and never stored).
+    bf16x8 qf[D / 16];
+    {
+      const bf16* qrow = static_cast<const bf16*>(p.q) + b * p.qs[0] + hq * p.qs[1] + tq * p.qs[2] + half * 8;
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = min(kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3), Tk - 1);
-        mv_next[mt][i] = kLog2e * load_mask(p.mask, p.mask_dtype, m_base + (int64_t)key * p.ms[3]);
+      for (int kk = 0; kk < D / 16; ++kk) {
+        u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + kk * 16);
+        if (!qvalid) raw = u32x4{0u, 0u, 0u, 0u};
+        qf[kk] = __builtin_bit_cast(bf16x8, raw);
       }
-  };
+    }
+    if (p.q_rms_eps >= 0.f) {
+      // Lane holds d = kk*16 + half*8 + e; lanes col and col+32 hold one row.
+      float ss = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          const float x = static_cast<float>(qf[kk][e2]);
+          ss += x * x;
+        }
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
+      // The weight slice of this lane as 16-byte vectors (16-byte aligned,
+      // checked on the host), all loads in flight together.
+      const bf16* wq = static_cast<const bf16*>(p.q_rms_weight);
+      bf16x8 wf[D / 16];
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+        if (wq) {
+          wf[kk] = *reinterpret_cast<const bf16x8*>(wq + kk * 16 + half * 8);
+        } else {
+#pragma unroll
+          for (int e2 = 0; e2 < 8; ++e2) wf[kk][e2] = static_cast<bf16>(1.f);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2)
+          qf[kk][e2] = static_cast<bf16>(static_cast<float>(qf[kk][e2]) * inv * static_cast<float>(wf[kk][e2]));
+    }
+    int64_t m_base = 0;
+    if constexpr (MASK) m_base = b * p.ms[0] + hq * p.ms[1] + tq * p.ms[2];
 
-  auto next_tile = [&](int t) -> int {
-    const uint64_t rest = t + 1 < 64 ? (vbits >> (t + 1)) : 0;
-    return rest ? t + 1 + __builtin_ctzll(rest) : -1;
-  };
+    const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+    const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+    const Loader kload(kp, p.ks[2], Tk, 0, lane), vload(vp, p.vs[2], Tk, 0, lane);
 
-  // Tile t from stage (kc, vc) while tile tn (if any) is issued into
-  // (kn, vn).  The restrict-qualified stage pointers scope this tile's
-  // accesses, so the compiler's LDS-DMA tracking does not make the operand
-  // reads wait for the next tile's loads.
-  auto body = [&](int t, int tn, const bf16* __restrict__ kc, const bf16* __restrict__ vc, bf16* __restrict__ kn,
-                  bf16* __restrict__ vn) __attribute__((always_inline)) {
-    const int kb = gtile(t) * kDN;
-    // This tile's mask values arrived with its K/V; the next tile's are
-    // issued after its DMA, so one in-order vmcnt wait covers this tile.
-    float mv[kMT][16];
-    if constexpr (MASK) {
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+    float b_run = -INFINITY, l_run = 0.f;
+
+    // Mask values of a tile in the S^T lane layout (keys past Tk clamped:
+    // they are masked by the key < Tk test), one register set per stage.
+    float mv0[kMT][16], mv1[kMT][16], mv2[kMT][16];
+    // Raw mask values of a tile in the S^T lane layout (scaled by log2(e) at
+    // use, so no arithmetic sits between a load and the next DMA).  With
+    // mask_vec4 (Tk a multiple of 4) a lane's keys come in runs of four
+    // consecutive keys: one 16-byte (f32) or 8-byte (bf16 / f16) load per
+    // run, runs past Tk clamped to the last one (those keys are masked by the
+    // key < Tk test).  Otherwise one element load per key.
+    const bool mvec = p.mask_vec4 != 0;
+    auto load_tile_mask = [&](int gt, float (&dst)[kMT][16]) __attribute__((always_inline)) {
+      const int kb = gt * kDN;
+      if (mvec) {
+#pragma unroll
+        for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int key = min(kb + mt * 32 + g * 8 + half * 4, Tk - 4);
+            const int64_t off = m_base + key;
+            if constexpr (MT == 1) {
+              const f32x4 v4 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.mask) + off);
+#pragma unroll
+              for (int e2 = 0; e2 < 4; ++e2) dst[mt][g * 4 + e2] = v4[e2];
+            } else {
+              const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.mask) + off);
+              dst[mt][g * 4 + 0] = __uint_as_float(raw.x);
+              dst[mt][g * 4 + 1] = __uint_as_float(raw.y);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = min(kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3), Tk - 1);
+            dst[mt][i] = load_mask_t<MT>(p.mask, m_base + (int64_t)key * p.ms[3]);
+          }
+      }
+    };
+    // Log2-domain mask value of S^T entry i from the raw registers.
+    auto mask_at = [&](const float (&raw)[kMT][16], int mt, int i) __attribute__((always_inline)) {
+      if constexpr (MT == 1) return kLog2e * raw[mt][i];
+      else {
+        float f;
+        if (mvec) {
+          // Four 16-bit values of run g packed in raw[g*4 .. g*4+1].
+          const uint32_t wd = __float_as_uint(raw[mt][(i >> 2) * 4 + ((i & 3) >> 1)]);
+          const uint16_t bits = (uint16_t)(wd >> (16 * (i & 1)));
+          f = MT == 2 ? __uint_as_float((uint32_t)bits << 16) : static_cast<float>(__builtin_bit_cast(_Float16, bits));
+        } else {
+          f = raw[mt][i];
+        }
+        return kLog2e * f;
+      }
+    };
+    auto issue = [&](int gt, bf16* kd, bf16* vd, float (&mvd)[kMT][16]) __attribute__((always_inline)) {
+      kload.load(gt, kd, 0);
+      vload.load(gt, vd, 0);
+      if constexpr (MASK) load_tile_mask(gt, mvd);
+    };
+    // Vector-memory operations one tile's loads add to the in-order count.
+    constexpr int kOps = 2 * Loader::LOADS + (MASK ? 16 * kMT : 0);
+    constexpr int kOpsVec = 2 * Loader::LOADS + (MASK ? 4 * kMT : 0);
+
+    // Tile list entry i from stage (kc, vc, mvc) while entry i+2 (if any) is
+    // issued into (kn, vn, mvn): three stages, two tiles in flight.  The
+    // restrict-qualified stage pointers scope this tile's accesses, so the
+    // compiler's LDS-DMA tracking does not make the operand reads wait for
+    // the later tiles' loads.
+    auto body = [&](int i, const bf16* __restrict__ kc, const bf16* __restrict__ vc, const float (&mvc)[kMT][16],
+                    bf16* __restrict__ kn, bf16* __restrict__ vn, float (&mvn)[kMT][16]) __attribute__((always_inline)) {
+      if (i - wb >= 64) {
+        wb += 64;
+        w0 = w1;
+        w1 = w2;
+        w2 = list_at(wb + 128 + lane);
+      }
+      const int kb = tile_at(i) * kDN;
+      float mv[kMT][16];
+      if constexpr (MASK) {
+#pragma unroll
+        for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+          for (int e2 = 0; e2 < 16; ++e2) mv[mt][e2] = mvc[mt][e2];
+      }
+      if (i + 2 < ntl) {
+        issue(tile_at(i + 2), kn, vn, mvn);
+        // The count field holds at most 63: waiting for one more operation
+        // than the two later tiles' loads is still correct.
+        if (mvec) wait_vm<(2 * kOpsVec < 64 ? 2 * kOpsVec : 63)>();
+        else wait_vm<(2 * kOps < 64 ? 2 * kOps : 63)>();
+      } else if (i + 1 < ntl) {
+        if (mvec) wait_vm<kOpsVec>();
+        else wait_vm<kOps>();
+      } else {
+        wait_vm<0>();
+      }
+      f32x16 sc[kMT];
+#pragma unroll
+      for (int mt = 0; mt < kMT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[mt][i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(kc) + k_addr[kk] +
+                                                            mt * 32 * D * 2);
+          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sc[mt], 0, 0, 0);
+        }
+      }
+      float mx = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mv[mt][i] = mv_next[mt][i];
-    }
-    if (tn >= 0) {
-      kload.load(gtile(tn), kn, 0);
-      vload.load(gtile(tn), vn, 0);
-      if constexpr (MASK) {
-        load_tile_mask(tn);
-        wait_vm<2 * Loader::LOADS + 16 * kMT>();
-      } else {
-        wait_vm<2 * Loader::LOADS>();
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+          float x = sc[mt][i] * sl2;
+          if constexpr (MASK) x += mask_at(mv, mt, i);
+          if (key >= Tk || (CAUSAL && key > tq)) x = -INFINITY;
+          sc[mt][i] = x;
+          mx = fmaxf(mx, x);
+        }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
       }
-    } else {
-      wait_vm<0>();
-    }
-    f32x16 s[kMT];
+      const bool need = mx > b_run + kSlack;
+      if (__ballot(need)) {
+        const float nb = need ? mx : b_run;
+        const float alpha = need ? __builtin_amdgcn_exp2f(b_run - nb) : 1.f;
+        b_run = nb;
+        l_run *= alpha;
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt) {
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(kc) + k_addr[kk] +
-                                                          mt * 32 * D * 2);
-        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[mt], 0, 0, 0);
+          for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
       }
-    }
-    float mx = -INFINITY;
+      const float nbase = b_run == -INFINITY ? 0.f : -b_run;
+      bf16x8 pb[kKS];
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
+      for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-        float x = s[mt][i] * sl2;
-        if constexpr (MASK) x += mv[mt][i];
-        if (key >= Tk || (CAUSAL && key > tq)) x = -INFINITY;
-        s[mt][i] = x;
-        mx = fmaxf(mx, x);
+        for (int i = 0; i < 16; ++i)
+          pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(__builtin_amdgcn_exp2f(sc[mt][i] + nbase));
+      {
+        const bf16x2 one = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
+        float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < kKS; ++j) {
+          const bf16x8 wv = pb[j];
+          l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[0], wv[1]}, one, l0, false);
+          l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[2], wv[3]}, one, l1, false);
+          l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[4], wv[5]}, one, l0, false);
+          l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[6], wv[7]}, one, l1, false);
+        }
+        l_run += l0 + l1;
       }
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    const bool need = mx > b_run + kSlack;
-    if (__ballot(need)) {
-      const float nb = need ? mx : b_run;
-      const float alpha = need ? __builtin_amdgcn_exp2f(b_run - nb) : 1.f;
-      b_run = nb;
-      l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+        for (int ks = 0; ks < kKS; ++ks) {
+          const char* vb = reinterpret_cast<const char*>(vc) + ks * 16 * D * 2;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + v_addr[dt][0]));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + v_addr[dt][1]));
+          const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
+        }
+    };
+
+    // The segment's tiles in list order, three per iteration (stages 0, 1,
+    // 2).  The stages of the previous segment are idle: its last body waited
+    // for every load and its reads precede this segment's first DMA in
+    // program order.
+    issue(tile_at(0), k0, v0, mv0);
+    if (ntl > 1) issue(tile_at(1), k1, v1, mv1);
+    for (int i = 0; i < ntl; i += 3) {
+      body(i, k0, v0, mv0, k2, v2, mv2);
+      if (i + 1 >= ntl) break;
+      body(i + 1, k1, v1, mv1, k0, v0, mv0);
+      if (i + 2 >= ntl) break;
+      body(i + 2, k2, v2, mv2, k1, v1, mv1);
     }
-    const float nbase = b_run == -INFINITY ? 0.f : -b_run;
-    bf16x8 pb[kKS];
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(__builtin_amdgcn_exp2f(s[mt][i] + nbase));
+
+    // Lanes col and col+32 hold the two halves of each row's keys.
+    float lt;
     {
-      const bf16x2 one = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
-      float l0 = 0.f, l1 = 0.f;
-#pragma unroll
-      for (int j = 0; j < kKS; ++j) {
-        const bf16x8 w = pb[j];
-        l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[0], w[1]}, one, l0, false);
-        l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[2], w[3]}, one, l1, false);
-        l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[4], w[5]}, one, l0, false);
-        l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[6], w[7]}, one, l1, false);
-      }
-      l_run += l0 + l1;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+      lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int ks = 0; ks < kKS; ++ks) {
-        const char* vb = reinterpret_cast<const char*>(vc) + ks * 16 * D * 2;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + v_addr[dt][0]));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + v_addr[dt][1]));
-        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
+    if (qvalid) {
+      float* part = p.partial + ((int64_t)(w + bhk) * R + rr) * (D + 2);
+      if (half == 0) {
+        part[0] = b_run;
+        part[1] = lt;
       }
-  };
-
-  int t = vbits ? __builtin_ctzll(vbits) : -1;
-  if (t >= 0) {
-    kload.load(gtile(t), k0, 0);
-    vload.load(gtile(t), v0, 0);
-    if constexpr (MASK) load_tile_mask(t);
-  }
-  // Two tiles per iteration (stage 0, stage 1), at most kMaxTiles tiles.
-  for (int it = 0; it < kMaxTiles && t >= 0; it += 2) {
-    int tn = next_tile(t);
-    body(t, tn, k0, v0, k1, v1);
-    if (tn < 0) break;
-    t = tn;
-    tn = next_tile(t);
-    body(t, tn, k1, v1, k0, v0);
-    t = tn;
-  }
-
-  // Lanes col and col+32 hold the two halves of each row's keys.
-  float lt;
-  {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-    lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-  }
-  if (!qvalid) return;
-  if (p.num_splits == 1) {
-    const float inv = 1.0f / lt;
-    bf16* orow = static_cast<bf16*>(p.out) + b * p.os[0] + hq * p.os[1] + tq * p.os[2];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
+        for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) orow[dt * 32 + gq * 8 + half * 4 + e] = static_cast<bf16>(o[dt][gq * 4 + e] * inv);
-  } else {
-    const int64_t rows_total = (int64_t)p.B * p.Hq * Tq;
-    const int64_t row = ((int64_t)b * p.Hq + hq) * Tq + tq;
-    float* part = p.partial + ((int64_t)split * rows_total + row) * (D + 2);
-    if (half == 0) {
-      part[0] = b_run;
-      part[1] = lt;
+          for (int e2 = 0; e2 < 4; ++e2) part[2 + dt * 32 + gq * 8 + half * 4 + e2] = o[dt][gq * 4 + e2];
     }
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) part[2 + dt * 32 + gq * 8 + half * 4 + e] = o[dt][gq * 4 + e];
+    s = seg_end;
+    P += cnt;
+    ++bhk;
+    while (s < e && bhk < BHk && p.tile_count[bhk] == 0) ++bhk;
   }
 }
 
-template <int D, bool MASK, bool CAUSAL>
+// Merges the partial (m, l, O) rows of each output row: one wavefront per
+// row.  The slots of bhk are w + bhk for the wavefronts w whose non-empty
+// range meets bhk's list; lanes load the slots' (m, l) 64 at a time and
+// reduce them, then every lane accumulates its features over the slots with
+// eight slots' loads in flight.  A row with no listed tile (every key
+// masked) is NaN, as the unfused softmax.
+template <typename OT, int D>
+__global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
+  constexpr int NQ = D / 64;  // features per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*Hq + h)*Tq + t
+  const int64_t rows_total = (int64_t)p.B * p.Hq * p.Tq;
+  if (row >= rows_total) return;
+  const int tq = (int)(row % p.Tq);
+  const int bh = (int)(row / p.Tq);
+  const int b = bh / p.Hq, h = bh % p.Hq;
+  const int hk = h / p.group;
+  const int bhk = b * p.Hkv + hk;
+  const int R = p.group * p.Tq;
+  const int rr = (h % p.group) * p.Tq + tq;
+  const int W = p.num_splits, BHk = p.B * p.Hkv;
+  // T = all listed tiles, P = those of the bhk before this one.
+  int64_t T = 0, P = 0;
+  for (int i0 = 0; i0 < BHk; i0 += 64) {
+    const int i = i0 + lane;
+    const int c = i < BHk ? p.tile_count[i] : 0;
+    int ct = c, cp = i < bhk ? c : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      ct += __shfl_xor(ct, off, 64);
+      cp += __shfl_xor(cp, off, 64);
+    }
+    T += ct;
+    P += cp;
+  }
+  const int cnt = p.tile_count[bhk];
+  OT* orow = static_cast<OT*>(p.out) + b * p.os[0] + h * p.os[1] + tq * p.os[2];
+  if (cnt == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) orow[lane + 64 * q] = from_f32<OT>(__builtin_nanf(""));
+    return;
+  }
+  // Wavefronts whose range [start(w), start(w+1)) meets [P, P + cnt).
+  int lo = (int)(P * W / T);
+  while (lo > 0 && range_start(lo, T, W) > P) --lo;
+  while (range_start(lo + 1, T, W) <= P) ++lo;
+  int hi = (int)((P + cnt - 1) * W / T);
+  while (hi + 1 < W && range_start(hi + 1, T, W) < P + cnt) ++hi;
+  while (range_start(hi, T, W) >= P + cnt) --hi;
+  const int nslot = hi - lo + 1;
+  auto slot_ptr = [&](int k) { return p.partial + ((int64_t)(lo + k + bhk) * R + rr) * (D + 2); };
+  // Lane k of a 64-slot chunk holds slot k0 + k: whether its wavefront's
+  // range is non-empty (the next lane's start differs) and its (m, l).
+  auto lane_slot = [&](int k0, float& mk, float& lk) {
+    const int k = k0 + lane;
+    const int64_t rs = range_start(lo + min(k, nslot), T, W);
+    const int64_t rn = __shfl_down(rs, 1, 64);
+    const int64_t re = lane == 63 ? range_start(lo + min(k + 1, nslot), T, W) : rn;
+    mk = -INFINITY;
+    lk = 0.f;
+    if (k < nslot && rs < re) {
+      const float2 ml = *reinterpret_cast<const float2*>(slot_ptr(k));
+      mk = ml.x;
+      lk = ml.y;
+    }
+  };
+  // Row maximum and the rescaled l over all slots.
+  float m = -INFINITY, l = 0.f, mk0 = -INFINITY;
+  for (int k0 = 0; k0 < nslot; k0 += 64) {
+    float mk, lk;
+    lane_slot(k0, mk, lk);
+    if (k0 == 0) mk0 = mk;
+    const float mc = group_max<64>(mk);
+    const float mn = fmaxf(m, mc);
+    const float bn = mn == -INFINITY ? 0.f : mn;
+    l = l * __builtin_amdgcn_exp2f(m - bn) + group_sum<64>(lk * __builtin_amdgcn_exp2f(mk - bn));
+    m = mn;
+  }
+  const float base = m == -INFINITY ? 0.f : m;
+  // O: each slot's features weighted by its uniform scale (read from the
+  // lane that holds it), sixteen slots' loads in flight.
+  float acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = 0.f;
+  for (int k0 = 0; k0 < nslot; k0 += 64) {
+    float mk = mk0, lk;
+    if (k0 > 0) lane_slot(k0, mk, lk);
+    const float sc = __builtin_amdgcn_exp2f(mk - base);  // 0 for empty slots
+    const int n = min(64, nslot - k0);
+    for (int j0 = 0; j0 < n; j0 += 16) {
+      float v[16][NQ];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float* pk = slot_ptr(k0 + min(j0 + u, n - 1));
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) v[u][q] = pk[2 + lane + 64 * q];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int su = j0 + u < n ? __builtin_amdgcn_readlane(__float_as_int(sc), j0 + u) : 0;
+        const float scu = __int_as_float(su);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) acc[q] = fmaf(v[u][q], scu, acc[q]);
+      }
+    }
+  }
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) orow[lane + 64 * q] = from_f32<OT>(acc[q] * inv);
+}
+
+template <int D, int MT, bool CAUSAL>
 int launch_t(const SdpaParams& p, hipStream_t s) {
-  dim3 grid((unsigned)(p.B * p.Hkv), (unsigned)p.num_splits);  // (kv heads, W)
-  hipLaunchKernelGGL((decode_mfma_kernel<D, MASK, CAUSAL>), grid, dim3(64), 0, s, p);
-  int rc = launch_status("decode_mfma_kernel");
-  if (rc != MFX_OK || p.num_splits == 1) return rc;
-  return launch_decode_combine(p, s);
+  hipLaunchKernelGGL((decode_tiles_kernel<MT, CAUSAL>), dim3((unsigned)(p.B * p.Hkv)), dim3(256), 0, s, p);
+  int rc = launch_status("decode_tiles_kernel");
+  if (rc != MFX_OK) return rc;
+  hipLaunchKernelGGL((decode_mfma_kernel<D, MT, CAUSAL>), dim3((unsigned)p.num_splits), dim3(64), 0, s, p);
+  if ((rc = launch_status("decode_mfma_kernel")) != MFX_OK) return rc;
+  const unsigned blocks = (unsigned)(((int64_t)p.B * p.Hq * p.Tq + 3) / 4);
+  hipLaunchKernelGGL((decode_bal_combine_kernel<bf16, D>), dim3(blocks), dim3(256), 0, s, p);
+  return launch_status("decode_bal_combine_kernel");
 }
 
 template <int D>
 int launch_d(const SdpaParams& p, hipStream_t s) {
   const bool m = p.mask != nullptr;
-  if (p.causal) return m ? launch_t<D, true, true>(p, s) : launch_t<D, false, true>(p, s);
-  return m ? launch_t<D, true, false>(p, s) : launch_t<D, false, false>(p, s);
+  const int mt = m ? mask_code(p.mask_dtype) : 0;
+  if (p.causal) {
+    switch (mt) {
+      case 1: return launch_t<D, 1, true>(p, s);
+      case 2: return launch_t<D, 2, true>(p, s);
+      case 3: return launch_t<D, 3, true>(p, s);
+      default: return launch_t<D, 0, true>(p, s);
+    }
+  }
+  switch (mt) {
+    case 1: return launch_t<D, 1, false>(p, s);
+    case 2: return launch_t<D, 2, false>(p, s);
+    case 3: return launch_t<D, 3, false>(p, s);
+    default: return launch_t<D, 0, false>(p, s);
+  }
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -386,7 +649,7 @@ bool decode_mfma_supports(const SdpaParams& p) {
   if (!(p.scale_log2 > 0.f)) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (p.group * p.Tq > 32) return false;
-  if ((int64_t)(p.Tk + kMaxTiles * kDN - 1) / (kMaxTiles * kDN) > 65535) return false;  // grid y = W
+  if ((int64_t)p.B * p.Hkv * ((p.Tk + kDN - 1) / kDN) >= (1LL << 31)) return false;  // tile lists
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v)) return false;
   for (int i = 0; i < 3; ++i)
@@ -396,7 +659,26 @@ bool decode_mfma_supports(const SdpaParams& p) {
 }
 
 int decode_mfma_tile() { return kDN; }
-int decode_mfma_max_tiles() { return kMaxTiles; }
+
+size_t decode_mfma_workspace(const SdpaParams& p, int W) {
+  const int64_t bhk = (int64_t)p.B * p.Hkv;
+  const int64_t cap = (p.Tk + kDN - 1) / kDN;
+  const size_t lists = (size_t)(bhk * cap + bhk) * sizeof(int);
+  const size_t parts = (size_t)(W + bhk) * p.group * p.Tq * (p.Dv + 2) * sizeof(float);
+  return (lists + 255) / 256 * 256 + parts;
+}
+
+void decode_mfma_bind(SdpaParams& p, int W, void* ws) {
+  const int64_t bhk = (int64_t)p.B * p.Hkv;
+  const int64_t cap = (p.Tk + kDN - 1) / kDN;
+  char* base = static_cast<char*>(ws);
+  p.tile_list = reinterpret_cast<int*>(base);
+  p.tile_count = p.tile_list + bhk * cap;
+  p.tiles_cap = (int)cap;
+  const size_t lists = (size_t)(bhk * cap + bhk) * sizeof(int);
+  p.partial = reinterpret_cast<float*>(base + (lists + 255) / 256 * 256);
+  p.num_splits = W;
+}
 
 int launch_decode_mfma(const SdpaParams& p, hipStream_t s) {
   return p.D == 128 ? launch_d<128>(p, s) : launch_d<64>(p, s);
