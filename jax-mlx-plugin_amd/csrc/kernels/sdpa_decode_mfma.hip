@@ -152,12 +152,29 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   const int Tq = p.Tq, R = p.group * Tq, Tk = p.Tk;
   const float sl2 = p.scale_log2;  // > 0 (checked on the host)
 
-  // Total listed tiles and this wavefront's range [s, e) of them: the
-  // counts are read 64 per vector load and summed across lanes (a scalar
-  // load per count would put ~BHk memory round trips before the first DMA).
+  // Total listed tiles and this wavefront's range [s, e) of them, then the
+  // bhk holding element s and the first element P of its list.  Up to
+  // 64 * kNC counts are held in registers (lane l of chunk c: bhk c*64 + l),
+  // all loaded in one round trip; larger grids read them 64 per load.
+  constexpr int kNC = 4;
+  const bool in_regs = BHk <= 64 * kNC;
+  int creg[kNC];
+#pragma unroll
+  for (int c = 0; c < kNC; ++c) creg[c] = in_regs && c * 64 + lane < BHk ? p.tile_count[c * 64 + lane] : 0;
+  auto chunk = [&](int i0) __attribute__((always_inline)) {
+    if (in_regs) {
+      const int c = i0 >> 6;
+      return c == 0 ? creg[0] : c == 1 ? creg[1] : c == 2 ? creg[2] : creg[3];
+    }
+    return i0 + lane < BHk ? p.tile_count[i0 + lane] : 0;
+  };
+  // Tile count of bhk i (uniform).
+  auto count_of = [&](int i) __attribute__((always_inline)) {
+    return in_regs ? __builtin_amdgcn_readlane(chunk(i & ~63), i & 63) : p.tile_count[i];
+  };
   int64_t T = 0;
   for (int i0 = 0; i0 < BHk; i0 += 64) {
-    int c = i0 + lane < BHk ? p.tile_count[i0 + lane] : 0;
+    int c = chunk(i0);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
     T += __builtin_amdgcn_readfirstlane(c);
@@ -165,12 +182,12 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   int64_t s = range_start(w, T, W);
   const int64_t e = range_start(w + 1, T, W);
   if (s >= e) return;
-  // The bhk holding element s and the first element of its list: inclusive
-  // prefix sums across lanes, then the first lane whose prefix passes s.
+  // Inclusive prefix sums across lanes, then the first lane whose prefix
+  // passes s.
   int bhk = 0;
   int64_t P = 0;
   for (int i0 = 0; i0 < BHk; i0 += 64) {
-    const int c = i0 + lane < BHk ? p.tile_count[i0 + lane] : 0;
+    const int c = chunk(i0);
     int incl = c;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -212,7 +229,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   // One segment per (batch, kv head) the range meets.  At most BHk
   // iterations; every iteration advances s by at least one tile.
   for (int guard = 0; guard < BHk && s < e; ++guard) {
-    const int cnt = p.tile_count[bhk];
+    const int cnt = count_of(bhk);
     const int64_t seg_end = e < P + cnt ? e : P + cnt;
     const int* lst = p.tile_list + (int64_t)bhk * p.tiles_cap + (s - P);
     const int ntl = (int)(seg_end - s);
@@ -493,7 +510,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     s = seg_end;
     P += cnt;
     ++bhk;
-    while (s < e && bhk < BHk && p.tile_count[bhk] == 0) ++bhk;
+    while (s < e && bhk < BHk && count_of(bhk) == 0) ++bhk;
   }
 }
 
