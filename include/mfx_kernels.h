@@ -370,6 +370,23 @@ typedef struct {
 
 int mfx_elementwise(const mfx_ew_program* prog, void* stream);
 
+/* Compiles, ahead of its first mfx_elementwise call, the native kernel of a
+ * program (hipRTC, gfx950): the instruction sequence, dtypes, dims and
+ * strides become constants of a generated kernel, cached per device.  Data
+ * pointers may be null here; their alignment, when given, selects the
+ * vector-load variant (16-byte aligned is assumed for null ones).
+ * mfx_elementwise uses the compiled kernel when one exists (compiling it on
+ * first use otherwise) and its interpreter for programs hipRTC rejects;
+ * MFX_EW_JIT=0 in the environment selects the interpreter always.
+ * No counterpart in the reference: it replaces the per-op MLX kernels that
+ * mx::compile fuses (src/jax_mlx_pjrt.cpp:9063-9081). */
+int mfx_ew_prepare(const mfx_ew_program* prog);
+
+/* Selects compiled kernels (on != 0, the default unless MFX_EW_JIT=0) or the
+ * interpreter for mfx_elementwise; returns the previous setting.  Process
+ * wide; for tests and measurements that compare the two paths. */
+int mfx_ew_jit_enable(int on);
+
 enum { MFX_RED_SUM = 0, MFX_RED_MAX = 1, MFX_RED_MIN = 2, MFX_RED_PROD = 3 };
 
 /* out[kept...] = init (op) reduce_{dims d with bit d of reduce_mask}(in),

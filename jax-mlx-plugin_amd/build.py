@@ -93,7 +93,7 @@ def build_kernels() -> Path:
     vscript = obj_dir / "exports.map"
     vscript.write_text("{ global: mfx_*; local: *; };\n")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
-          f"-Wl,--version-script={vscript}", "-L/opt/rocm/lib", "-lrocblas",
+          f"-Wl,--version-script={vscript}", "-L/opt/rocm/lib", "-lrocblas", "-lhiprtc",
           "-Wl,-rpath,/opt/rocm/lib", "-o", str(tmp)])
     os.replace(tmp, out)
     return out

@@ -446,26 +446,31 @@ void collapse(mfx_ew_program& p) {
 }
 
 }  // namespace
-}  // namespace mfx
 
-extern "C" {
+// Native kernels generated per program (ew_jit.cpp).
+bool ew_jit_launch(const mfx_ew_program& p, hipStream_t s, int* rc);
+int ew_jit_prepare(const mfx_ew_program& p);
 
-int mfx_elementwise(const mfx_ew_program* prog_in, void* stream) {
-  using namespace mfx;
+namespace {
+
+// Validates prog_in and returns in p the program to run: dims collapsed
+// where every input's strides allow it (contiguous outputs only).  Sets
+// numel; returns MFX_OK or an error.
+int normalise(const mfx_ew_program* prog_in, mfx_ew_program& p, int64_t& numel, bool need_ptrs) {
   if (!prog_in) return fail(MFX_E_INVALID, "null program");
-  mfx_ew_program p = *prog_in;
+  p = *prog_in;
   if (p.rank < 0 || p.rank > MFX_MAX_RANK) return fail(MFX_E_INVALID, "rank out of range");
   if (p.num_inputs < 0 || p.num_inputs > MFX_EW_MAX_INPUTS) return fail(MFX_E_INVALID, "too many inputs");
   if (p.num_instrs <= 0 || p.num_instrs > MFX_EW_MAX_INSTRS) return fail(MFX_E_INVALID, "bad instruction count");
   if (p.result < 0 || p.result >= MFX_EW_MAX_REGS) return fail(MFX_E_INVALID, "bad result register");
-  if (!p.out || !valid_dtype(p.out_dtype)) return fail(MFX_E_INVALID, "bad output");
-  int64_t numel = 1;
+  if ((need_ptrs && !p.out) || !valid_dtype(p.out_dtype)) return fail(MFX_E_INVALID, "bad output");
+  numel = 1;
   for (int d = 0; d < p.rank; ++d) {
     if (p.dims[d] < 0) return fail(MFX_E_INVALID, "negative dim");
     numel *= p.dims[d];
   }
   for (int i = 0; i < p.num_inputs; ++i)
-    if (!p.inputs[i].data || !valid_dtype(p.inputs[i].dtype)) return fail(MFX_E_INVALID, "bad input");
+    if ((need_ptrs && !p.inputs[i].data) || !valid_dtype(p.inputs[i].dtype)) return fail(MFX_E_INVALID, "bad input");
   bool written[MFX_EW_MAX_REGS] = {};
   for (int pc = 0; pc < p.num_instrs; ++pc) {
     const mfx_ew_instr& in = p.code[pc];
@@ -481,15 +486,39 @@ int mfx_elementwise(const mfx_ew_program* prog_in, void* stream) {
     written[in.dst] = true;
   }
   if (!written[p.result]) return fail(MFX_E_INVALID, "result register never written");
-  if (numel == 0) return MFX_OK;
   int strided = 0;
   for (int d = 0; d < p.rank; ++d) strided |= p.out_strides[d] != 0;
-  if (strided) {
-    // Out-of-place layout: keep the dims as given (no collapsing).
-  } else {
-    collapse(p);
-  }
+  // A strided (out-of-place) output keeps the dims as given.
+  if (!strided) collapse(p);
+  return MFX_OK;
+}
+
+}  // namespace
+}  // namespace mfx
+
+extern "C" {
+
+int mfx_ew_prepare(const mfx_ew_program* prog_in) {
+  using namespace mfx;
+  mfx_ew_program p;
+  int64_t numel = 0;
+  const int rc = normalise(prog_in, p, numel, false);
+  if (rc != MFX_OK || numel == 0) return rc;
+  return ew_jit_prepare(p);
+}
+
+int mfx_elementwise(const mfx_ew_program* prog_in, void* stream) {
+  using namespace mfx;
+  mfx_ew_program p;
+  int64_t numel = 0;
+  int rc = normalise(prog_in, p, numel, true);
+  if (rc != MFX_OK || numel == 0) return rc;
+  int strided = 0;
+  for (int d = 0; d < p.rank; ++d) strided |= p.out_strides[d] != 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The program's own compiled kernel when hipRTC builds it; the
+  // interpreter below otherwise.
+  if (ew_jit_launch(p, s, &rc)) return rc;
   // Four elements per thread when the output is contiguous with an inner
   // dim that is a multiple of four.
   const int last = p.rank - 1;
