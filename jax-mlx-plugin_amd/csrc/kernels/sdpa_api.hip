@@ -66,18 +66,11 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
 
   if (p.Tq <= 4 && decode_mfma_supports(p)) {
     // W wavefronts split the listed (visible) tiles of all kv heads into
-    // equal ranges: as many as stay resident at once (three 48 KB-LDS
-    // workgroups per CU at d = 128, six at d = 64, on 256 CUs), at most one
-    // per tile.
+    // equal ranges: as many as stay resident at once, at most one per tile.
     out.kind = Kind::kDecodeMfma;
     const int64_t tiles = (int64_t)p.B * p.Hkv * ((p.Tk + decode_mfma_tile() - 1) / decode_mfma_tile());
-    const int64_t resident = p.D == 128 ? 768 : 1536;
+    const int64_t resident = decode_mfma_resident(p);
     out.decode_waves = (int)(tiles < resident ? tiles : resident);
-    // Vector mask loads: contiguous keys, every row start 4-element aligned,
-    // Tk a whole number of runs of four keys.
-    const int msz = p.mask_dtype == MFX_F32 ? 4 : 2;
-    p.mask_vec4 = p.mask && p.ms[3] == 1 && p.Tk % 4 == 0 && (uintptr_t)p.mask % (4 * msz) == 0 &&
-                  p.ms[0] % 4 == 0 && p.ms[1] % 4 == 0 && p.ms[2] % 4 == 0;
     out.partial_bytes = decode_mfma_workspace(p, out.decode_waves);
     return MFX_OK;
   }

@@ -30,9 +30,6 @@ struct SdpaParams {
   int* tile_list;
   int* tile_count;
   int tiles_cap;
-  // Mask rows are contiguous along keys and 4-element aligned (so a lane's
-  // four consecutive keys are one vector load).
-  int mask_vec4;
   // Optional: row log-sum-exp of the scaled scores in log2 units,
   // lse[(b * Hq + h) * Tq + i] = log2(sum_j exp2(s_ij)), written by the
   // flash and generic kernels when non-null (the backward pass reads it).
@@ -81,6 +78,9 @@ bool flash_f32_supports(const SdpaParams& p);
 bool decode_supports(const SdpaParams& p);
 bool decode_mfma_supports(const SdpaParams& p);
 int decode_mfma_tile();  // keys per tile of the MFMA decode
+// Wavefronts of the MFMA decode that are resident at once (its LDS per
+// workgroup against the 160 KB of a CU, on 256 CUs).
+int decode_mfma_resident(const SdpaParams& p);
 // Workspace bytes of the MFMA decode with W wavefronts: tile lists, counts and
 // the (W + B*Hkv) * R partial rows.
 size_t decode_mfma_workspace(const SdpaParams& p, int W);

@@ -24,8 +24,14 @@
 // slots of the wavefronts whose range meets that bhk.
 //
 // K/V tiles stream through three swizzled LDS stages by asynchronous LDS-DMA
-// loads; while one tile is computed, the next two are in flight (the kernel
-// is bound by bytes in flight per CU, which the 160 KB of LDS caps).
+// loads; while one tile is computed, the next two are in flight.  The
+// additive mask of a tile travels the same way: its values are gathered by
+// LDS-DMA (one 4-byte slot per key and row, 16-bit types zero-extended) into
+// the tail of the tile's V stage, so every load of the stream is an LDS-DMA
+// whose completion the explicit vmcnt waits account for.  (Mask values
+// loaded into registers instead make the compiler's wait insertion lose
+// track of them across the rotating stages and drain the whole queue before
+// each tile.)
 //
 // Optional fused RMSNorm of the query rows (reference chain rms_norm -> sdpa
 // of GQA decode): q is normalised in fp32 and rounded to bf16 before it is
@@ -38,13 +44,58 @@ namespace mfx {
 namespace {
 
 using tiles::kSlack;
-using tiles::lds_s16x4_t;
+using tiles::lds_void_t;
 using tiles::s16x4;
 using tiles::tile_swz;
 
-constexpr int kDN = 32;  // keys per tile: three stages = 48 KB of LDS per workgroup, three per CU
+constexpr int kDN = 32;  // keys per tile: three stages = 48 KB of LDS per workgroup at d = 128
 constexpr int kMT = kDN / 32;
 constexpr int kKS = kDN / 16;
+constexpr int kStages = 3;
+
+// Mask slots (4 bytes each) per stage: the tile's keys once when the mask is
+// the same for every query row of a kv head (MB), else once per row (up to
+// 32 rows).  One LDS-DMA instruction fills 64 slots.
+template <int MT, bool MB>
+constexpr int mask_slots() { return MT == 0 ? 0 : (MB ? 64 : 32 * kDN); }
+
+// LDS bytes of one workgroup of the main kernel.
+template <int D, int MT, bool MB>
+constexpr int stage_lds_bytes() { return kStages * (2 * kDN * D * 2 + 4 * mask_slots<MT, MB>()); }
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
+
+// s_waitcnt lgkmcnt(0) that the values read by inline-asm LDS loads depend
+// on, so no use of them is scheduled before it.  The memory clobber keeps
+// later writes to the stage (the next LDS-DMA into it) after the reads.
+__device__ __forceinline__ void lgkm_wait_tied(bf16x8 (&a)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7])
+               :
+               : "memory");
+}
+__device__ __forceinline__ void lgkm_wait_tied(bf16x8 (&a)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : : "memory");
+}
+__device__ __forceinline__ void lgkm_wait_tied(s16x4 (&v)[4][2][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]), "+v"(v[1][0][0]),
+                 "+v"(v[1][0][1]), "+v"(v[1][1][0]), "+v"(v[1][1][1]), "+v"(v[2][0][0]), "+v"(v[2][0][1]),
+                 "+v"(v[2][1][0]), "+v"(v[2][1][1]), "+v"(v[3][0][0]), "+v"(v[3][0][1]), "+v"(v[3][1][0]),
+                 "+v"(v[3][1][1])
+               :
+               : "memory");
+}
+__device__ __forceinline__ void lgkm_wait_tied(s16x4 (&v)[2][2][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]), "+v"(v[1][0][0]),
+                 "+v"(v[1][0][1]), "+v"(v[1][1][0]), "+v"(v[1][1][1])
+               :
+               : "memory");
+}
 
 // s_waitcnt vmcnt(N) with the other counters left alone (N < 64).
 template <int N>
@@ -134,16 +185,20 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(SdpaParams p) {
 // First element of wavefront w's range of the concatenated tile lists.
 __device__ __forceinline__ int64_t range_start(int w, int64_t T, int W) { return (int64_t)w * T / W; }
 
-template <int D, int MT, bool CAUSAL>
+template <int D, int MT, bool MB, bool CAUSAL>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   constexpr bool MASK = MT != 0;
   using Loader = tiles::TileLoader<D, kDN, 1>;
+  constexpr int kMS = mask_slots<MT, MB>();
+  constexpr int kMI = kMS / 64;  // mask LDS-DMA instructions per tile
+  // Each V stage is followed by the tile's mask slots (kMS 4-byte slots).
+  constexpr int kVN = kDN * D + 2 * kMS;
   __shared__ __attribute__((aligned(16))) bf16 k0[kDN * D];
-  __shared__ __attribute__((aligned(16))) bf16 v0[kDN * D];
+  __shared__ __attribute__((aligned(16))) bf16 v0[kVN];
   __shared__ __attribute__((aligned(16))) bf16 k1[kDN * D];
-  __shared__ __attribute__((aligned(16))) bf16 v1[kDN * D];
+  __shared__ __attribute__((aligned(16))) bf16 v1[kVN];
   __shared__ __attribute__((aligned(16))) bf16 k2[kDN * D];
-  __shared__ __attribute__((aligned(16))) bf16 v2[kDN * D];
+  __shared__ __attribute__((aligned(16))) bf16 v2[kVN];
 
   const int lane = threadIdx.x;
   const int half = lane >> 5, col = lane & 31;
@@ -151,6 +206,12 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   const int BHk = p.B * p.Hkv;
   const int Tq = p.Tq, R = p.group * Tq, Tk = p.Tk;
   const float sl2 = p.scale_log2;  // > 0 (checked on the host)
+  // Bytes the mask spans (strides >= 0 and the span < 2^31, checked on the
+  // host): the extent of the mask gathers' buffer resource.
+  [[maybe_unused]] const int mspan = MASK ? (int)(((int64_t)(p.B - 1) * p.ms[0] + (int64_t)(p.Hq - 1) * p.ms[1] +
+                                  (int64_t)(p.Tq - 1) * p.ms[2] + (int64_t)(Tk - 1) * p.ms[3] + 1) *
+                                 (MT == 1 ? 4 : 2))
+                            : 0;
 
   // Total listed tiles and this wavefront's range [s, e) of them, then the
   // bhk holding element s and the first element P of its list.  Up to
@@ -249,51 +310,34 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
     const int hq = hk * p.group + rr / Tq, tq = rr % Tq;
 
-    // This lane's query column (rows past R are zero and never stored).
-    bf16x8 qf[D / 16];
+    // This lane's query column and RMSNorm weight slice: loaded here and
+    // used once the segment's first tiles are in flight, so their round trip
+    // overlaps the tiles'.  Lane holds d = kk*16 + half*8 + e; lanes col and
+    // col+32 hold one row.  (The weight is 16-byte aligned, checked on the
+    // host.)
+    const bool qnorm = p.q_rms_eps >= 0.f;
+    const bf16* wq = static_cast<const bf16*>(p.q_rms_weight);
+    bf16x8 qf[D / 16], wf[D / 16];
     {
       const bf16* qrow = static_cast<const bf16*>(p.q) + b * p.qs[0] + hq * p.qs[1] + tq * p.qs[2] + half * 8;
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-        u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + kk * 16);
-        if (!qvalid) raw = u32x4{0u, 0u, 0u, 0u};
-        qf[kk] = __builtin_bit_cast(bf16x8, raw);
+      for (int kk = 0; kk < D / 16; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + kk * 16);
+      if (qnorm && wq) {
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) wf[kk] = *reinterpret_cast<const bf16x8*>(wq + kk * 16 + half * 8);
       }
     }
-    if (p.q_rms_eps >= 0.f) {
-      // Lane holds d = kk*16 + half*8 + e; lanes col and col+32 hold one row.
-      float ss = 0.f;
+    // Mask element offset of the row each lane gathers in each mask
+    // instruction: slot j*64 + lane holds key (lane & 31) of row 2j + half
+    // (row 0 with MB; rows past R repeat row R - 1).  Offsets fit 31 bits
+    // (checked on the host).
+    [[maybe_unused]] constexpr int esz = MT == 1 ? 4 : 2;
+    int mrow[kMI > 0 ? kMI : 1];
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)
-#pragma unroll
-        for (int e2 = 0; e2 < 8; ++e2) {
-          const float x = static_cast<float>(qf[kk][e2]);
-          ss += x * x;
-        }
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
-      // The weight slice of this lane as 16-byte vectors (16-byte aligned,
-      // checked on the host), all loads in flight together.
-      const bf16* wq = static_cast<const bf16*>(p.q_rms_weight);
-      bf16x8 wf[D / 16];
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-        if (wq) {
-          wf[kk] = *reinterpret_cast<const bf16x8*>(wq + kk * 16 + half * 8);
-        } else {
-#pragma unroll
-          for (int e2 = 0; e2 < 8; ++e2) wf[kk][e2] = static_cast<bf16>(1.f);
-        }
-      }
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)
-#pragma unroll
-        for (int e2 = 0; e2 < 8; ++e2)
-          qf[kk][e2] = static_cast<bf16>(static_cast<float>(qf[kk][e2]) * inv * static_cast<float>(wf[kk][e2]));
+    for (int j = 0; j < kMI; ++j) {
+      const int r = MB ? 0 : min(2 * j + half, R - 1);
+      mrow[j] = (int)(b * p.ms[0] + (hk * p.group + r / Tq) * p.ms[1] + (r % Tq) * p.ms[2]);
     }
-    int64_t m_base = 0;
-    if constexpr (MASK) m_base = b * p.ms[0] + hq * p.ms[1] + tq * p.ms[2];
 
     const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
     const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
@@ -306,77 +350,46 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
     float b_run = -INFINITY, l_run = 0.f;
 
-    // Mask values of a tile in the S^T lane layout (keys past Tk clamped:
-    // they are masked by the key < Tk test), one register set per stage.
-    float mv0[kMT][16], mv1[kMT][16], mv2[kMT][16];
-    // Raw mask values of a tile in the S^T lane layout (scaled by log2(e) at
-    // use, so no arithmetic sits between a load and the next DMA).  With
-    // mask_vec4 (Tk a multiple of 4) a lane's keys come in runs of four
-    // consecutive keys: one 16-byte (f32) or 8-byte (bf16 / f16) load per
-    // run, runs past Tk clamped to the last one (those keys are masked by the
-    // key < Tk test).  Otherwise one element load per key.
-    const bool mvec = p.mask_vec4 != 0;
-    auto load_tile_mask = [&](int gt, float (&dst)[kMT][16]) __attribute__((always_inline)) {
-      const int kb = gt * kDN;
-      if (mvec) {
+    // Mask gather of tile gt into the slots after V stage vd: instruction j
+    // writes slots j*64 .. j*64+63.  Keys past Tk are clamped to the last
+    // key (they are masked by the key < Tk test).  The resource spans the
+    // mask's extent, so every gathered offset is range-checked.
+    auto issue_mask = [&](int gt, bf16* vd) __attribute__((always_inline)) {
+#if defined(__HIP_DEVICE_COMPILE__)
+      if constexpr (MASK) {
+        const int64_t key = min(gt * kDN + col, Tk - 1);
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.mask), (short)0,
+                                                                             mspan, 0x00020000);
+        char* md = reinterpret_cast<char*>(vd + kDN * D);
 #pragma unroll
-        for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int key = min(kb + mt * 32 + g * 8 + half * 4, Tk - 4);
-            const int64_t off = m_base + key;
-            if constexpr (MT == 1) {
-              const f32x4 v4 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.mask) + off);
-#pragma unroll
-              for (int e2 = 0; e2 < 4; ++e2) dst[mt][g * 4 + e2] = v4[e2];
-            } else {
-              const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.mask) + off);
-              dst[mt][g * 4 + 0] = __uint_as_float(raw.x);
-              dst[mt][g * 4 + 1] = __uint_as_float(raw.y);
-            }
-          }
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = min(kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3), Tk - 1);
-            dst[mt][i] = load_mask_t<MT>(p.mask, m_base + (int64_t)key * p.ms[3]);
-          }
-      }
-    };
-    // Log2-domain mask value of S^T entry i from the raw registers.
-    auto mask_at = [&](const float (&raw)[kMT][16], int mt, int i) __attribute__((always_inline)) {
-      if constexpr (MT == 1) return kLog2e * raw[mt][i];
-      else {
-        float f;
-        if (mvec) {
-          // Four 16-bit values of run g packed in raw[g*4 .. g*4+1].
-          const uint32_t wd = __float_as_uint(raw[mt][(i >> 2) * 4 + ((i & 3) >> 1)]);
-          const uint16_t bits = (uint16_t)(wd >> (16 * (i & 1)));
-          f = MT == 2 ? __uint_as_float((uint32_t)bits << 16) : static_cast<float>(__builtin_bit_cast(_Float16, bits));
-        } else {
-          f = raw[mt][i];
+        for (int j = 0; j < kMI; ++j) {
+          const uint32_t voff = (uint32_t)((mrow[j] + key * p.ms[3]) * esz);
+          if constexpr (esz == 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(md + j * 256), 4, voff, 0, 0, 0);
+          else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(md + j * 256), 2, voff, 0, 0, 0);
         }
-        return kLog2e * f;
       }
+#endif
     };
-    auto issue = [&](int gt, bf16* kd, bf16* vd, float (&mvd)[kMT][16]) __attribute__((always_inline)) {
+    auto issue = [&](int gt, bf16* kd, bf16* vd) __attribute__((always_inline)) {
       kload.load(gt, kd, 0);
       vload.load(gt, vd, 0);
-      if constexpr (MASK) load_tile_mask(gt, mvd);
+      issue_mask(gt, vd);
     };
     // Vector-memory operations one tile's loads add to the in-order count.
-    constexpr int kOps = 2 * Loader::LOADS + (MASK ? 16 * kMT : 0);
-    constexpr int kOpsVec = 2 * Loader::LOADS + (MASK ? 4 * kMT : 0);
+    constexpr int kOps = 2 * Loader::LOADS + kMI;
+    // This lane's mask row in the slots (rows past R read row 0; their
+    // columns are never stored).
+    const int mslot = MB ? half * 4 : rr * kDN + half * 4;
 
-    // Tile list entry i from stage (kc, vc, mvc) while entry i+2 (if any) is
-    // issued into (kn, vn, mvn): three stages, two tiles in flight.  The
+    // Tile list entry i from stage (kc, vc) while entry i+2 (if any) is
+    // issued into (kn, vn): three stages, two tiles in flight.  The
     // restrict-qualified stage pointers scope this tile's accesses, so the
     // compiler's LDS-DMA tracking does not make the operand reads wait for
     // the later tiles' loads.
-    auto body = [&](int i, const bf16* __restrict__ kc, const bf16* __restrict__ vc, const float (&mvc)[kMT][16],
-                    bf16* __restrict__ kn, bf16* __restrict__ vn, float (&mvn)[kMT][16]) __attribute__((always_inline)) {
+    auto body = [&](int i, const bf16* __restrict__ kc, const bf16* __restrict__ vc, bf16* __restrict__ kn,
+                    bf16* __restrict__ vn) __attribute__((always_inline)) {
       if (i - wb >= 64) {
         wb += 64;
         w0 = w1;
@@ -384,36 +397,68 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         w2 = list_at(wb + 128 + lane);
       }
       const int kb = tile_at(i) * kDN;
-      float mv[kMT][16];
-      if constexpr (MASK) {
-#pragma unroll
-        for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-          for (int e2 = 0; e2 < 16; ++e2) mv[mt][e2] = mvc[mt][e2];
-      }
       if (i + 2 < ntl) {
-        issue(tile_at(i + 2), kn, vn, mvn);
+        issue(tile_at(i + 2), kn, vn);
         // The count field holds at most 63: waiting for one more operation
         // than the two later tiles' loads is still correct.
-        if (mvec) wait_vm<(2 * kOpsVec < 64 ? 2 * kOpsVec : 63)>();
-        else wait_vm<(2 * kOps < 64 ? 2 * kOps : 63)>();
+        wait_vm<(2 * kOps < 64 ? 2 * kOps : 63)>();
       } else if (i + 1 < ntl) {
-        if (mvec) wait_vm<kOpsVec>();
-        else wait_vm<kOps>();
+        wait_vm<kOps>();
       } else {
         wait_vm<0>();
       }
+      // Log2-domain mask values of this lane's 16 keys (S^T entry i holds
+      // key (i >> 2) * 8 + half * 4 + (i & 3)).
+      float mv[kMT][16];
+      if constexpr (MASK) {
+        const uint32_t* mc = reinterpret_cast<const uint32_t*>(vc + kDN * D) + mslot;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const u32x4 w4 = *reinterpret_cast<const u32x4*>(mc + g * 8);
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            float f;
+            if constexpr (MT == 1) f = __uint_as_float(w4[e2]);
+            else if constexpr (MT == 2) f = __uint_as_float(w4[e2] << 16);
+            else f = static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)w4[e2]));
+            mv[0][g * 4 + e2] = kLog2e * f;
+          }
+        }
+      }
+      // K operand reads, all issued before one wait, as inline asm: the
+      // vmcnt wait above already covers this stage's loads, and the
+      // compiler's LDS-DMA tracking, which does not tell this stage from the
+      // one just issued, would also wait for the later tile's K loads.
       f32x16 sc[kMT];
 #pragma unroll
       for (int mt = 0; mt < kMT; ++mt) {
+        bf16x8 ka[D / 16];
+        const uint32_t kbase = lds_addr(kc) + mt * 32 * D * 2;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk)
+          asm volatile("ds_read_b128 %0, %1" : "=v"(ka[kk]) : "v"(kbase + k_addr[kk]));
+        lgkm_wait_tied(ka);
 #pragma unroll
         for (int i = 0; i < 16; ++i) sc[mt][i] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(kc) + k_addr[kk] +
-                                                            mt * 32 * D * 2);
-          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sc[mt], 0, 0, 0);
-        }
+        for (int kk = 0; kk < D / 16; ++kk)
+          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk], qf[kk], sc[mt], 0, 0, 0);
+      }
+      // V^T operand reads (transposing), issued now so that their latency
+      // overlaps the softmax; inline asm for the same reason as the K reads.
+      static_assert(kKS == 2, "two 16-key halves per tile");
+      s16x4 vr[D / 32][kKS][2];
+      {
+        const uint32_t vbase = lds_addr(vc);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vr[dt][0][h]) : "v"(vbase + v_addr[dt][h]));
+            asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                         : "=v"(vr[dt][1][h])
+                         : "v"(vbase + v_addr[dt][h]), "i"(16 * D * 2));
+          }
       }
       float mx = -INFINITY;
 #pragma unroll
@@ -422,7 +467,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         for (int i = 0; i < 16; ++i) {
           const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
           float x = sc[mt][i] * sl2;
-          if constexpr (MASK) x += mask_at(mv, mt, i);
+          if constexpr (MASK) x += mv[mt][i];
           if (key >= Tk || (CAUSAL && key > tq)) x = -INFINITY;
           sc[mt][i] = x;
           mx = fmaxf(mx, x);
@@ -462,14 +507,13 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         }
         l_run += l0 + l1;
       }
+      lgkm_wait_tied(vr);
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int ks = 0; ks < kKS; ++ks) {
-          const char* vb = reinterpret_cast<const char*>(vc) + ks * 16 * D * 2;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + v_addr[dt][0]));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vb + v_addr[dt][1]));
-          const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          const bf16x8 a =
+              __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[dt][ks][0], vr[dt][ks][1], 0, 1, 2, 3, 4, 5, 6, 7));
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
         }
     };
@@ -478,14 +522,39 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     // 2).  The stages of the previous segment are idle: its last body waited
     // for every load and its reads precede this segment's first DMA in
     // program order.
-    issue(tile_at(0), k0, v0, mv0);
-    if (ntl > 1) issue(tile_at(1), k1, v1, mv1);
+    issue(tile_at(0), k0, v0);
+    if (ntl > 1) issue(tile_at(1), k1, v1);
+    // Rows past R are zero (never stored); optional RMSNorm in fp32, rounded
+    // to bf16 as the unfused graph rounds its output.
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      if (!qvalid) qf[kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    if (qnorm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          const float x = static_cast<float>(qf[kk][e2]);
+          ss += x * x;
+        }
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          const float wv = wq ? static_cast<float>(wf[kk][e2]) : 1.f;
+          qf[kk][e2] = static_cast<bf16>(static_cast<float>(qf[kk][e2]) * inv * wv);
+        }
+    }
     for (int i = 0; i < ntl; i += 3) {
-      body(i, k0, v0, mv0, k2, v2, mv2);
+      body(i, k0, v0, k2, v2);
       if (i + 1 >= ntl) break;
-      body(i + 1, k1, v1, mv1, k0, v0, mv0);
+      body(i + 1, k1, v1, k0, v0);
       if (i + 2 >= ntl) break;
-      body(i + 2, k2, v2, mv2, k1, v1, mv1);
+      body(i + 2, k2, v2, k1, v1);
     }
 
     // Lanes col and col+32 hold the two halves of each row's keys.
@@ -518,8 +587,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 // row.  The slots of bhk are w + bhk for the wavefronts w whose non-empty
 // range meets bhk's list; lanes load the slots' (m, l) 64 at a time and
 // reduce them, then every lane accumulates its features over the slots with
-// eight slots' loads in flight.  A row with no listed tile (every key
-// masked) is NaN, as the unfused softmax.
+// sixteen slots' loads in flight (the first sixteen issued together with the
+// (m, l) loads).  A row with no listed tile (every key masked) is NaN, as the
+// unfused softmax.
 template <typename OT, int D>
 __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   constexpr int NQ = D / 64;  // features per lane
@@ -535,12 +605,24 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   const int R = p.group * p.Tq;
   const int rr = (h % p.group) * p.Tq + tq;
   const int W = p.num_splits, BHk = p.B * p.Hkv;
-  // T = all listed tiles, P = those of the bhk before this one.
+  // T = all listed tiles, P = those of the bhks before this one, cnt =
+  // this bhk's.  The counts are read 256 at a time: four loads per lane in
+  // flight together.
+  const int cnt = p.tile_count[bhk];
   int64_t T = 0, P = 0;
-  for (int i0 = 0; i0 < BHk; i0 += 64) {
-    const int i = i0 + lane;
-    const int c = i < BHk ? p.tile_count[i] : 0;
-    int ct = c, cp = i < bhk ? c : 0;
+  for (int i0 = 0; i0 < BHk; i0 += 256) {
+    int c[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * 64 + lane;
+      c[u] = i < BHk ? p.tile_count[i] : 0;
+    }
+    int ct = 0, cp = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ct += c[u];
+      cp += i0 + u * 64 + lane < bhk ? c[u] : 0;
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       ct += __shfl_xor(ct, off, 64);
@@ -549,7 +631,6 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
     T += ct;
     P += cp;
   }
-  const int cnt = p.tile_count[bhk];
   OT* orow = static_cast<OT*>(p.out) + b * p.os[0] + h * p.os[1] + tq * p.os[2];
   if (cnt == 0) {
 #pragma unroll
@@ -565,6 +646,15 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   while (range_start(hi, T, W) >= P + cnt) --hi;
   const int nslot = hi - lo + 1;
   auto slot_ptr = [&](int k) { return p.partial + ((int64_t)(lo + k + bhk) * R + rr) * (D + 2); };
+  // The features of the first 16 slots, loaded before (and in flight with)
+  // the slots' (m, l) below.
+  float vf[16][NQ];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const float* pk = slot_ptr(min(u, nslot - 1));
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) vf[u][q] = pk[2 + lane + 64 * q];
+  }
   // Lane k of a 64-slot chunk holds slot k0 + k: whether its wavefront's
   // range is non-empty (the next lane's start differs) and its (m, l).
   auto lane_slot = [&](int k0, float& mk, float& lk) {
@@ -594,16 +684,29 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   }
   const float base = m == -INFINITY ? 0.f : m;
   // O: each slot's features weighted by its uniform scale (read from the
-  // lane that holds it), sixteen slots' loads in flight.
+  // lane that holds it).  A slot of weight 0 adds nothing; an empty range's
+  // slot was never written, so its contents are not read into the sum
+  // (0 * NaN).
   float acc[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) acc[q] = 0.f;
+  auto accumulate = [&](const float (&v)[16][NQ], float sc, int j0, int n) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int su = j0 + u < n ? __builtin_amdgcn_readlane(__float_as_int(sc), j0 + u) : 0;
+      const float scu = __int_as_float(su);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) acc[q] = scu != 0.f ? fmaf(v[u][q], scu, acc[q]) : acc[q];
+    }
+  };
+  accumulate(vf, __builtin_amdgcn_exp2f(mk0 - base), 0, min(64, nslot));
+  // Slots past the first 16, sixteen slots' loads in flight.
   for (int k0 = 0; k0 < nslot; k0 += 64) {
     float mk = mk0, lk;
     if (k0 > 0) lane_slot(k0, mk, lk);
     const float sc = __builtin_amdgcn_exp2f(mk - base);  // 0 for empty slots
     const int n = min(64, nslot - k0);
-    for (int j0 = 0; j0 < n; j0 += 16) {
+    for (int j0 = k0 == 0 ? 16 : 0; j0 < n; j0 += 16) {
       float v[16][NQ];
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
@@ -611,13 +714,7 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
 #pragma unroll
         for (int q = 0; q < NQ; ++q) v[u][q] = pk[2 + lane + 64 * q];
       }
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int su = j0 + u < n ? __builtin_amdgcn_readlane(__float_as_int(sc), j0 + u) : 0;
-        const float scu = __int_as_float(su);
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) acc[q] = fmaf(v[u][q], scu, acc[q]);
-      }
+      accumulate(v, sc, j0, n);
     }
   }
   const float inv = 1.0f / l;
@@ -625,16 +722,29 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   for (int q = 0; q < NQ; ++q) orow[lane + 64 * q] = from_f32<OT>(acc[q] * inv);
 }
 
-template <int D, int MT, bool CAUSAL>
+// Whether every query row of a kv head sees the same mask row (the mask is
+// broadcast over heads of a group and over query positions, or those have
+// extent 1).
+bool mask_rows_shared(const SdpaParams& p) {
+  return (p.ms[1] == 0 || p.group == 1) && (p.ms[2] == 0 || p.Tq == 1);
+}
+
+template <int D, int MT, bool MB, bool CAUSAL>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   hipLaunchKernelGGL((decode_tiles_kernel<MT, CAUSAL>), dim3((unsigned)(p.B * p.Hkv)), dim3(256), 0, s, p);
   int rc = launch_status("decode_tiles_kernel");
   if (rc != MFX_OK) return rc;
-  hipLaunchKernelGGL((decode_mfma_kernel<D, MT, CAUSAL>), dim3((unsigned)p.num_splits), dim3(64), 0, s, p);
+  hipLaunchKernelGGL((decode_mfma_kernel<D, MT, MB, CAUSAL>), dim3((unsigned)p.num_splits), dim3(64), 0, s, p);
   if ((rc = launch_status("decode_mfma_kernel")) != MFX_OK) return rc;
   const unsigned blocks = (unsigned)(((int64_t)p.B * p.Hq * p.Tq + 3) / 4);
   hipLaunchKernelGGL((decode_bal_combine_kernel<bf16, D>), dim3(blocks), dim3(256), 0, s, p);
   return launch_status("decode_bal_combine_kernel");
+}
+
+template <int D, int MT, bool CAUSAL>
+int launch_m(const SdpaParams& p, hipStream_t s) {
+  if constexpr (MT == 0) return launch_t<D, 0, true, CAUSAL>(p, s);
+  else return mask_rows_shared(p) ? launch_t<D, MT, true, CAUSAL>(p, s) : launch_t<D, MT, false, CAUSAL>(p, s);
 }
 
 template <int D>
@@ -643,18 +753,24 @@ int launch_d(const SdpaParams& p, hipStream_t s) {
   const int mt = m ? mask_code(p.mask_dtype) : 0;
   if (p.causal) {
     switch (mt) {
-      case 1: return launch_t<D, 1, true>(p, s);
-      case 2: return launch_t<D, 2, true>(p, s);
-      case 3: return launch_t<D, 3, true>(p, s);
-      default: return launch_t<D, 0, true>(p, s);
+      case 1: return launch_m<D, 1, true>(p, s);
+      case 2: return launch_m<D, 2, true>(p, s);
+      case 3: return launch_m<D, 3, true>(p, s);
+      default: return launch_m<D, 0, true>(p, s);
     }
   }
   switch (mt) {
-    case 1: return launch_t<D, 1, false>(p, s);
-    case 2: return launch_t<D, 2, false>(p, s);
-    case 3: return launch_t<D, 3, false>(p, s);
-    default: return launch_t<D, 0, false>(p, s);
+    case 1: return launch_m<D, 1, false>(p, s);
+    case 2: return launch_m<D, 2, false>(p, s);
+    case 3: return launch_m<D, 3, false>(p, s);
+    default: return launch_m<D, 0, false>(p, s);
   }
+}
+
+template <int D>
+int lds_bytes_d(const SdpaParams& p) {
+  if (!p.mask) return stage_lds_bytes<D, 0, true>();
+  return mask_rows_shared(p) ? stage_lds_bytes<D, 1, true>() : stage_lds_bytes<D, 1, false>();
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -672,10 +788,27 @@ bool decode_mfma_supports(const SdpaParams& p) {
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8) return false;
   if (p.q_rms_eps >= 0.f && p.q_rms_weight && !aligned16(p.q_rms_weight)) return false;
+  if (p.mask) {
+    // The mask is gathered through a buffer resource with 32-bit offsets.
+    int64_t span = 1;
+    const int64_t ext[4] = {p.B, p.Hq, p.Tq, p.Tk};
+    for (int i = 0; i < 4; ++i) {
+      if (p.ms[i] < 0) return false;
+      span += (ext[i] - 1) * p.ms[i];
+    }
+    if (span * (p.mask_dtype == MFX_F32 ? 4 : 2) >= (1LL << 31)) return false;
+  }
   return true;
 }
 
 int decode_mfma_tile() { return kDN; }
+
+int decode_mfma_resident(const SdpaParams& p) {
+  // Workgroups (one wavefront each) that fit the 160 KB of LDS of a CU, on
+  // 256 CUs.
+  const int lds = p.D == 128 ? lds_bytes_d<128>(p) : lds_bytes_d<64>(p);
+  return 256 * (160 * 1024 / lds);
+}
 
 size_t decode_mfma_workspace(const SdpaParams& p, int W) {
   const int64_t bhk = (int64_t)p.B * p.Hkv;

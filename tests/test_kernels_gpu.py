@@ -385,6 +385,38 @@ def test_sdpa_decode_mfma_per_row_mask_and_holes(cuda, nat, oracle):
     check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 0.09, mask=mask), "bf16")
 
 
+@pytest.mark.parametrize("mdt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("rows", ["shared", "per_row"])
+@pytest.mark.parametrize("D,tk", [(64, 777), (128, 1030)])
+def test_sdpa_decode_mfma_mask_dtypes_and_strides(cuda, nat, oracle, mdt, rows, D, tk):
+    """Additive masks of every element type on the MFMA decode (the kernel
+    gathers them as 2- or 4-byte loads into LDS): one mask row shared by all
+    query rows of a kv head, or one per (head, query position); Tk ragged
+    against the 32-key tile; keys at stride 2 (a strided view); -inf runs,
+    holes and finite biases; the per-row case also causal."""
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv = 2, 8, 2
+    tq = 1 if rows == "shared" else 2
+    q, k, v = make_qkv(cuda, 32, (B, Hq, tq, D), (B, Hkv, tk, D), cuda.bfloat16)
+    shape = (B, 1, 1, 2 * tk) if rows == "shared" else (B, Hq, tq, 2 * tk)
+    base = rng.standard_normal(shape) * 0.5
+    base[..., 100:260] = -np.inf                    # keys 50..129 of the strided view
+    base[1, ..., 2 * (tk // 2):] = -np.inf          # batch 1 sees half the cache
+    base[0, ..., 22::22] = -np.inf                  # holes (every 11th key of the view from 11)
+    td = {"bf16": cuda.bfloat16, "f16": cuda.float16, "f32": cuda.float32}[mdt]
+    full = dev(cuda, base, td)
+    maskd = full[..., ::2]
+    assert maskd.stride(-1) == 2
+    mask = host(maskd.float())                      # the values the kernel sees
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd) == "decode_splitkv_mfma"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, mask=maskd)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, mask=mask), "bf16")
+    if rows == "per_row":
+        out_c = nat.sdpa(q, k, v, scale=D ** -0.5, mask=maskd, causal=True)
+        ref_c = oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=True, mask=mask)
+        check_sdpa(out_c, ref_c, "bf16")
+
+
 def test_sdpa_decode_mfma_fully_masked_row_is_nan(cuda, nat):
     q, k, v = make_qkv(cuda, 24, (1, 4, 1, 64), (1, 2, 300, 64), cuda.bfloat16)
     mask = cuda.zeros(1, 4, 1, 300, device="cuda")
