@@ -417,6 +417,24 @@ def test_sdpa_decode_mfma_mask_dtypes_and_strides(cuda, nat, oracle, mdt, rows, 
         check_sdpa(out_c, ref_c, "bf16")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_sdpa_decode_mfma_ranges_across_many_lists(cuda, nat, oracle, D):
+    """More listed tiles than resident wavefronts and (batch, kv head) lists
+    shorter than a wavefront's range: ranges start mid-list and span two or
+    three lists (several partial segments per wavefront, merged per row by
+    the combine); lengths vary per batch, some lists hold a single tile."""
+    rng = np.random.default_rng(41)
+    B, Hq, Hkv, tk = 64, 8, 8, 517
+    q, k, v = make_qkv(cuda, 42, (B, Hq, 1, D), (B, Hkv, tk, D), cuda.bfloat16)
+    lens = rng.integers(1, tk, size=B, endpoint=True)
+    lens[:4] = [1, 32, 33, tk]
+    mask = np.where(np.arange(tk)[None] < lens[:, None], 0.0, -np.inf).reshape(B, 1, 1, tk)
+    maskd = dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd) == "decode_splitkv_mfma"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, mask=maskd)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, mask=mask), "bf16")
+
+
 def test_sdpa_decode_mfma_fully_masked_row_is_nan(cuda, nat):
     q, k, v = make_qkv(cuda, 24, (1, 4, 1, 64), (1, 2, 300, 64), cuda.bfloat16)
     mask = cuda.zeros(1, 4, 1, 300, device="cuda")
