@@ -14,9 +14,10 @@ Timing: HIP events recorded on the stream the kernels are launched on (torch's
 current stream, whose handle the C-ABI receives), W untimed warmup steps,
 then exactly K steps bracketed by torch.cuda.synchronize().
 
-cpu_baseline: the fp64 C oracle (oracle/liboracle.so, single thread) on a
-bounded sample of the same workload -- one of the 128 (batch, head) pairs,
-all 2048 query rows -- scaled to TFLOP/s.
+cpu_baseline: torch-CPU F.scaled_dot_product_attention(is_causal=True) on the
+same config-3 tensors with all the host threads torch uses (BASELINE's
+fallback when JAX is absent; not the same module).  `extra` also holds the
+fp64 C oracle (oracle/liboracle.so, one thread) on one (batch, head) pair.
 """
 from __future__ import annotations
 
@@ -101,7 +102,51 @@ def bench_config3(torch, native, steps, warmup):
     }
 
 
-def cpu_baseline_config3(q, k, v):
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_config3_torch(torch, q, k, v, warmup=5, reps=20, cap_s=30.0):
+    """BASELINE's CPU fallback (JAX is absent on the box): torch-CPU
+    F.scaled_dot_product_attention(is_causal=True) on the same config-3
+    tensors (bf16, full [4,32,2048,128]) on all the host threads torch uses.
+    Not the same module as the GPU path, so labelled as such.  `warmup`
+    untimed calls, then the median of `reps` calls, stopping early at `cap_s`
+    seconds of timed calls."""
+    import statistics
+
+    qc, kc, vc = (t.cpu() for t in (q, k, v))
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    for _ in range(warmup):
+        sdpa(qc, kc, vc, is_causal=True)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < reps and time.perf_counter() - t_start < cap_s:
+        t0 = time.perf_counter()
+        sdpa(qc, kc, vc, is_causal=True)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    flops = sdpa_causal_flops(4, 32, 2048, 128)
+    return {
+        "value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+        "kind": "torch-cpu",
+        "sample": f"torch-CPU F.scaled_dot_product_attention(is_causal=True), bf16, the full config-3 tensors "
+                  f"(not the same module: JAX is absent); {warmup} warm-up calls, median of {len(times)} calls "
+                  f"(cap {cap_s:.0f} s) = {med * 1e3:.1f} ms",
+        "threads": torch.get_num_threads(), "affinity_cpus": len(os.sched_getaffinity(0)),
+        "cpu_count": os.cpu_count(), "cpu_model": cpu_model(),
+    }
+
+
+def cpu_oracle_config3(q, k, v):
+    """The fp64 C oracle (test infrastructure, one thread) on one of the 128
+    (batch, head) pairs of config 3, scaled to TFLOP/s."""
     import numpy as np
 
     import oracle_api as oracle
@@ -211,15 +256,16 @@ def bench_config2(torch, native, steps, warmup):
 def bench_config5(torch, native, steps, warmup, rotate=2):
     import numpy as np
 
+    # BASELINE order from default_rng(5): q, k, v, lengths (as the parity
+    # test draws them); the rotation's second K/V set is drawn after them.
     rng = np.random.default_rng(5)
     B, Hq, Hkv, d, S = 16, 32, 8, 128, 8192
-    q = torch.from_numpy(rng.standard_normal((B, Hq, 1, d)).astype(np.float32)).cuda().bfloat16()
-    kvs = []
-    for _ in range(rotate):
-        k = torch.randn(B, Hkv, S, d, device="cuda", dtype=torch.bfloat16)
-        v = torch.randn(B, Hkv, S, d, device="cuda", dtype=torch.bfloat16)
-        kvs.append((k, v))
+    draw = lambda shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda().bfloat16()  # noqa
+    q = draw((B, Hq, 1, d))
+    kvs = [(draw((B, Hkv, S, d)), draw((B, Hkv, S, d)))]
     lens = rng.integers(1024, 8192, size=B, endpoint=True)
+    while len(kvs) < rotate:
+        kvs.append((draw((B, Hkv, S, d)), draw((B, Hkv, S, d))))
     mask = torch.from_numpy(np.where(np.arange(S)[None] < lens[:, None], 0.0, -np.inf)
                             .reshape(B, 1, 1, S).astype(np.float32)).cuda()
     out = torch.empty_like(q)
@@ -245,11 +291,11 @@ def bench_config4(torch, steps, warmup):
     """4-layer pre-LN transformer forward (f32, d 512, 8 heads, MLP 2048,
     x [32,256,512]) compiled from StableHLO text and run through the PJRT C
     API (Client_Compile, LoadedExecutable_Execute) on device-resident
-    buffers.  Xavier-uniform weights, zero biases, unit LayerNorm scales.
-    Timed with the host clock around `steps` back-to-back Executes (the
-    plugin runs them in order on its own stream) and one final event wait."""
-    import math
-
+    buffers.  Xavier-uniform weights, zero biases, unit LayerNorm scales,
+    drawn from default_rng(4) (mlir_modules.config4_inputs, the inputs of
+    the config-4 parity test).  Timed with the host clock around `steps`
+    back-to-back Executes (the plugin runs them in order on its own stream)
+    and one final event wait."""
     import mlir_modules
     from jax_mlx_amd import pjrt
 
@@ -258,18 +304,8 @@ def bench_config4(torch, steps, warmup):
     t0 = time.perf_counter()
     exe = client.compile(mlir_modules.transformer_module(layers=layers, B=B, T=T, d=d, heads=heads, mlp=mlp))
     compile_s = time.perf_counter() - t0
-    gen = torch.Generator(device="cuda").manual_seed(4)
-
-    def xavier(fi, fo):
-        a = math.sqrt(6.0 / (fi + fo))
-        return (torch.rand(fi, fo, device="cuda", generator=gen) * 2 - 1) * a
-
-    tensors = [torch.randn(B, T, d, device="cuda", generator=gen)]
-    for _ in range(layers):
-        tensors += [torch.ones(d, device="cuda"), torch.zeros(d, device="cuda"), xavier(d, 3 * d),
-                    torch.zeros(3 * d, device="cuda"), xavier(d, d), torch.zeros(d, device="cuda"),
-                    torch.ones(d, device="cuda"), torch.zeros(d, device="cuda"), xavier(d, mlp),
-                    torch.zeros(mlp, device="cuda"), xavier(mlp, d), torch.zeros(d, device="cuda")]
+    arrays = mlir_modules.config4_inputs(seed=4, layers=layers, B=B, T=T, d=d, mlp=mlp)
+    tensors = [torch.from_numpy(a).cuda() for a in arrays]
     torch.cuda.synchronize()
     bufs = [client.buffer_view(t) for t in tensors]
     for _ in range(warmup):
@@ -415,18 +451,27 @@ def main() -> int:
                    "kernel": c3["kernel"]},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic("flash_bf16_config3.md")},
+                     "traffic": profiled_traffic("flash_bf16_config3.md"),
+                     "traffic_source": "profiles/flash_bf16_config3.md: rocprofv3 FETCH_SIZE and WRITE_SIZE of "
+                                       "this kernel, calibrated against a plain copy; read from the committed "
+                                       "profile, not measured in this run"},
     }
     log(f"  {c3['avg_ms'] * 1e3:.1f} us/step, {achieved:.1f} TFLOP/s")
+    oracle_cpu = None
     if not args.no_cpu:
-        log("cpu_baseline: fp64 oracle on 1 of 128 heads")
-        line["cpu_baseline"] = cpu_baseline_config3(q, k, v)
+        log("cpu_baseline: torch-CPU SDPA on the config-3 tensors")
+        line["cpu_baseline"] = cpu_baseline_config3_torch(torch, q, k, v)
+        if not args.no_extra:
+            log("fp64 C oracle on 1 of 128 heads")
+            oracle_cpu = cpu_oracle_config3(q, k, v)
     del q, k, v
     torch.cuda.empty_cache()
 
     if not args.no_extra:
         extra = {"config3_median_us": round(c3["median_ms"] * 1e3, 2),
                  "config3_tflops_full_square_count": round(c3["tflops_full_square_count"], 2)}
+        if oracle_cpu:
+            extra["cpu_fp64_oracle_config3"] = oracle_cpu
         log("config 1: LayerNorm f32 [8,128,512]")
         extra["config1_layer_norm"] = bench_config1(torch, native, 200, 20)
         log("LayerNorm HBM sweep")

@@ -32,6 +32,7 @@
 #include <unordered_map>
 
 #include "common.h"
+#include "ew_index.h"
 
 namespace mfx {
 
@@ -41,7 +42,7 @@ int ew_jit_prepare(const mfx_ew_program& p);
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = kEwThreads;
 
 struct JitKernel {
   hipModule_t module = nullptr;
@@ -238,7 +239,7 @@ std::string gen_source(const mfx_ew_program& p, const Layout& L, int64_t& work_i
   const int64_t inner = R > 0 ? p.dims[last] : 1;
   const int64_t inner_chunks = V == 4 ? inner / 4 : inner;
   work_items = V == 4 ? numel / 4 : numel;
-  const bool wide = work_items >= (1LL << 31) - kThreads * 65536LL;
+  const bool wide = ew_needs_wide_index(work_items);
   const char* IDX = wide ? "long long" : "int";
   std::ostringstream o;
   o << "typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));\n"
@@ -429,8 +430,7 @@ bool ew_jit_launch(const mfx_ew_program& p, hipStream_t s, int* rc) {
   for (int i = 0; i < p.num_inputs; ++i) args.in[i] = p.inputs[i].data;
   size_t size = sizeof(args);
   void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
-  const int64_t blocks64 = (k->work_items + kThreads - 1) / kThreads;
-  const unsigned blocks = (unsigned)(blocks64 < (1 << 20) ? (blocks64 > 0 ? blocks64 : 1) : (1 << 20));
+  const unsigned blocks = (unsigned)ew_blocks(k->work_items);
   const hipError_t e = hipModuleLaunchKernel(k->fn, blocks, 1, 1, kThreads, 1, 1, 0, s, nullptr, config);
   *rc = e == hipSuccess ? MFX_OK : hip_fail(e, "mfx_ew_kernel");
   return true;

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(SdpaBwdParams p, float* 
 // Log2-domain score of (query i of head h, key j) given the dot product.
 __device__ __forceinline__ float bwd_score(const SdpaBwdParams& p, float dot, int b, int h, int i, int j) {
   float x = dot * p.scale_log2;
-  if (p.mask) x += kLog2e * load_mask(p.mask, p.mask_dtype, b * p.ms[0] + h * p.ms[1] + i * p.ms[2] + j * p.ms[3]);
+  if (p.mask) x += mask_log2(load_mask(p.mask, p.mask_dtype, b * p.ms[0] + h * p.ms[1] + i * p.ms[2] + j * p.ms[3]));
   return x;
 }
 

@@ -205,9 +205,9 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
         float x = s[i] * sl2;
         if constexpr (MASK) {
           if (q < Tq && key < Tk)
-            x += kLog2e * load_mask(p.mask, p.mask_dtype,
+            x += mask_log2(load_mask(p.mask, p.mask_dtype,
                                     b * p.ms[0] + (int64_t)(hk * G + g) * p.ms[1] + (int64_t)q * p.ms[2] +
-                                        (int64_t)key * p.ms[3]);
+                                        (int64_t)key * p.ms[3]));
         }
         float pr = __builtin_amdgcn_exp2f(x - lse4[e]);
         if constexpr (EDGE) {
@@ -362,9 +362,9 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
       float x = s[i] * sl2;
       if constexpr (MASK) {
         if (qi < Tq && key < Tk)
-          x += kLog2e * load_mask(p.mask, p.mask_dtype,
+          x += mask_log2(load_mask(p.mask, p.mask_dtype,
                                   b * p.ms[0] + (int64_t)h * p.ms[1] + (int64_t)qi * p.ms[2] +
-                                      (int64_t)key * p.ms[3]);
+                                      (int64_t)key * p.ms[3]));
       }
       float pr = __builtin_amdgcn_exp2f(x - lse);
       if constexpr (EDGE) {

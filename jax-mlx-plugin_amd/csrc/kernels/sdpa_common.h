@@ -99,6 +99,17 @@ __device__ __forceinline__ float load_mask_t(const void* m, int64_t off) {
   else return static_cast<float>(static_cast<const _Float16*>(m)[off]);
 }
 
+// An additive-mask value in log2 units.  Finite values below kMaskMin are
+// raised to it first, so the product with log2(e) stays finite: JAX masks with
+// the finite value -0.7 * FLT_MAX (and finfo.min is common), whose product with
+// log2(e) would round to -inf.  With the clamp a row whose keys all carry such
+// a value has equal scores and returns the mean of V, as jnp.where-then-softmax
+// does; with -inf it would be 0/0.  -inf itself (and NaN) pass through.
+constexpr float kMaskMin = -2.3e38f;  // above -FLT_MAX / log2(e) = -2.3586e38
+__device__ __forceinline__ float mask_log2(float m) {
+  return kLog2e * ((m < kMaskMin && m != -INFINITY) ? kMaskMin : m);
+}
+
 // Loads one additive-mask element as fp32.
 __device__ __forceinline__ float load_mask(const void* m, int dt, int64_t off) {
   if (dt == MFX_F32) return static_cast<const float*>(m)[off];

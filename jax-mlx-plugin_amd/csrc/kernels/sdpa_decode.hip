@@ -126,8 +126,8 @@ __global__ __launch_bounds__(kNT) void decode_kernel(SdpaParams p) {
         float x = (key < kend && r < rows) ? 0.f : -INFINITY;
         if constexpr (MASK) {
           if (x == 0.f)
-            x = kLog2e * load_mask(p.mask, p.mask_dtype,
-                                   b * p.ms[0] + hq[r] * p.ms[1] + tr[r] * p.ms[2] + key * p.ms[3]);
+            x = mask_log2(load_mask(p.mask, p.mask_dtype,
+                                   b * p.ms[0] + hq[r] * p.ms[1] + tr[r] * p.ms[2] + key * p.ms[3]));
         }
         if (CAUSAL && key > tr[r]) x = -INFINITY;
         mv[u][r] = x;

@@ -421,7 +421,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
             if constexpr (MT == 1) f = __uint_as_float(w4[e2]);
             else if constexpr (MT == 2) f = __uint_as_float(w4[e2] << 16);
             else f = static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)w4[e2]));
-            mv[0][g * 4 + e2] = kLog2e * f;
+            mv[0][g * 4 + e2] = mask_log2(f);
           }
         }
       }

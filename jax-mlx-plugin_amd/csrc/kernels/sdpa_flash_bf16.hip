@@ -162,8 +162,8 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
         if constexpr (MASK) {
           x *= sl2;
           if (qi < Tq && key < Tk)
-            x += kLog2e * load_mask(p.mask, p.mask_dtype,
-                                    b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]);
+            x += mask_log2(load_mask(p.mask, p.mask_dtype,
+                                    b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]));
         }
         if constexpr (EDGE) {
           if (key >= Tk || (CAUSAL && key > qi)) x = -INFINITY;

@@ -141,8 +141,8 @@ __global__ __launch_bounds__(kNT, 2) void flash_f32_kernel(SdpaParams p) {
         const int key = kb + (i >> 2) * 8 + half * 4 + (i & 3);
         if constexpr (MASK) {
           if (qi < Tq && key < Tk)
-            x += kLog2e * load_mask(p.mask, p.mask_dtype,
-                                    b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]);
+            x += mask_log2(load_mask(p.mask, p.mask_dtype,
+                                    b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]));
         }
         if (edge && (key >= Tk || (CAUSAL && key > qi))) x = -INFINITY;
         s[i] = x;

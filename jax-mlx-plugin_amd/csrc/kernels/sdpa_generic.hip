@@ -57,8 +57,8 @@ __global__ __launch_bounds__(64) void generic_kernel(SdpaParams p) {
       for (int d = 0; d < D; ++d) acc += q_lds[d] * to_f32(krow[d]);
       s = acc * p.scale_log2;
       if (p.mask)
-        s += kLog2e * load_mask(p.mask, p.mask_dtype,
-                                b * p.ms[0] + h * p.ms[1] + t * p.ms[2] + key * p.ms[3]);
+        s += mask_log2(load_mask(p.mask, p.mask_dtype,
+                                b * p.ms[0] + h * p.ms[1] + t * p.ms[2] + key * p.ms[3]));
     }
     const float mx = group_max<64>(s);
     const float m_new = fmaxf(m, mx);

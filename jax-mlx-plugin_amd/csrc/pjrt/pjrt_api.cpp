@@ -263,15 +263,38 @@ struct PJRT_Buffer {
   void* on_delete_arg = nullptr;
   std::vector<int64_t> minor_to_major;
 
+  // Set when the memory's release waits for the last external reference,
+  // and when Buffer_Destroy came while one was still held (the object then
+  // lives until that reference is dropped).
+  bool release_pending = false;
+  bool destroyed = false;
+  std::mutex mu;
+
+  // Marks the buffer deleted and releases its memory: owned memory returns to
+  // the client's stream-ordered pool (later work on the stream reuses it only
+  // after the work already queued), a view's on_delete callback runs once the
+  // work queued on the device's stream has finished reading it.  While
+  // external references (DLPack and the like) are held, the release waits for
+  // the last one to be dropped.
   void free_memory() {
+    std::lock_guard<std::mutex> g(mu);
     if (deleted) return;
     deleted = true;
+    if (ext_refs.load() > 0) {
+      release_pending = true;
+      return;
+    }
+    release_locked();
+  }
+  void release_locked() {
     if (owned && ptr) {
       client->release(device->ordinal, ptr, bytes);
     } else if (on_delete) {
+      if (device && device->stream) (void)hipStreamSynchronize(device->stream);
       on_delete(ptr, on_delete_arg);
     }
     ptr = nullptr;
+    release_pending = false;
   }
 };
 
@@ -1185,8 +1208,16 @@ PJRT_Error* LoadedExecutable_Execute(PJRT_LoadedExecutable_Execute_Args* args) {
 PJRT_Error* Buffer_Destroy(PJRT_Buffer_Destroy_Args* args) {
   CHECK_ARGS(PJRT_Buffer_Destroy_Args, buffer);
   if (!args->buffer) return nullptr;
-  args->buffer->free_memory();
-  delete args->buffer;
+  PJRT_Buffer* b = args->buffer;
+  b->free_memory();
+  {
+    std::lock_guard<std::mutex> g(b->mu);
+    if (b->release_pending) {
+      b->destroyed = true;  // freed by the last DecreaseExternalReferenceCount
+      return nullptr;
+    }
+  }
+  delete b;
   return nullptr;
 }
 PJRT_Error* Buffer_ElementType(PJRT_Buffer_ElementType_Args* args) {
@@ -1351,14 +1382,26 @@ PJRT_Error* Buffer_UnsafePointer(PJRT_Buffer_UnsafePointer_Args* args) {
 }
 PJRT_Error* Buffer_IncreaseExternalReferenceCount(PJRT_Buffer_IncreaseExternalReferenceCount_Args* args) {
   CHECK_ARGS(PJRT_Buffer_IncreaseExternalReferenceCount_Args, buffer);
+  std::lock_guard<std::mutex> g(args->buffer->mu);
+  if (args->buffer->deleted)
+    return make_error(PJRT_Error_Code_FAILED_PRECONDITION, "external reference to a deleted buffer");
   args->buffer->ext_refs++;
   return nullptr;
 }
 PJRT_Error* Buffer_DecreaseExternalReferenceCount(PJRT_Buffer_DecreaseExternalReferenceCount_Args* args) {
   CHECK_ARGS(PJRT_Buffer_DecreaseExternalReferenceCount_Args, buffer);
-  if (args->buffer->ext_refs.load() <= 0)
-    return make_error(PJRT_Error_Code_FAILED_PRECONDITION, "external reference count is already zero");
-  args->buffer->ext_refs--;
+  PJRT_Buffer* b = args->buffer;
+  bool destroy = false;
+  {
+    std::lock_guard<std::mutex> g(b->mu);
+    if (b->ext_refs.load() <= 0)
+      return make_error(PJRT_Error_Code_FAILED_PRECONDITION, "external reference count is already zero");
+    if (--b->ext_refs == 0 && b->release_pending) {
+      b->release_locked();
+      destroy = b->destroyed;
+    }
+  }
+  if (destroy) delete b;
   return nullptr;
 }
 PJRT_Error* Buffer_OpaqueDeviceMemoryDataPointer(PJRT_Buffer_OpaqueDeviceMemoryDataPointer_Args* args) {

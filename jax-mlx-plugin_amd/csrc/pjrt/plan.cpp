@@ -1134,12 +1134,25 @@ class Planner {
         a.mask_dtype = mfx_dtype(ty(mask).dtype);
       }
     }
-    // Workspace (split-KV partials) from the arena, sized with aligned placeholders.
-    mfx_sdpa_args probe = a;
-    probe.q = probe.k = probe.v = probe.out = (void*)0x10000;
-    probe.mask = mask >= 0 ? (void*)0x10000 : nullptr;
-    probe.q_rms_weight = wq >= 0 ? (void*)0x10000 : nullptr;
-    size_t ws = mfx_sdpa_workspace_size(&probe);
+    // Workspace (split-KV partials, a normalised copy of q) from the arena.
+    // The kernel is chosen at run time from the operands' alignment, so the
+    // size is the larger of two probes: every buffer 256-byte aligned (arena
+    // and pool buffers) plus each operand's element offset, and every operand
+    // one element off 16-byte alignment (a caller's view of odd alignment).
+    const int pb = dtype_bytes(dt);
+    const int64_t mb = mask >= 0 ? dtype_bytes(ty(mask).dtype) : 0;
+    size_t ws = 0;
+    for (int64_t skew : {(int64_t)0, (int64_t)1}) {
+      mfx_sdpa_args probe = a;
+      const uintptr_t base = 0x10000;
+      probe.q = (void*)(base + (offs[0] + skew) * pb);
+      probe.k = (void*)(base + (offs[1] + skew) * pb);
+      probe.v = (void*)(base + (offs[2] + skew) * pb);
+      probe.out = (void*)base;
+      probe.mask = mask >= 0 ? (void*)(base + (moff + skew) * mb) : nullptr;
+      probe.q_rms_weight = wq >= 0 ? (void*)base : nullptr;
+      ws = std::max(ws, mfx_sdpa_workspace_size(&probe));
+    }
     int ws_v = -1;
     if (ws > 0) {
       Type wt;

@@ -1242,6 +1242,12 @@ int rewrite_custom_calls(Ctx& c, RewriteStats& st) {
       json_number(cfg, "scale", scale);
       int64_t B = qt.dims[0], T = qt.dims[1], N = qt.dims[2], H = qt.dims[3];
       int64_t S = kt.dims[1], K = kt.dims[2];
+      const Type& vt = c.ty(n.in[2]);
+      if (vt.rank() != 4 || kt.dims[0] != B || kt.dims[3] != H || vt.dims[0] != B || vt.dims[1] != S ||
+          vt.dims[2] != K || K <= 0 || N % K != 0)
+        throw ParseError("mlx_sdpa operand shapes do not agree");
+      if (c.ty(n.out[0]).dims != std::vector<int64_t>{B, T, N, vt.dims[3]})
+        throw ParseError("mlx_sdpa result shape does not agree with q and v");
       Node f;
       f.op = "mfx.sdpa";
       f.in = n.in;

@@ -229,6 +229,25 @@ def layer_norm_module(shape=(8, 128, 512), eps=1e-5, dt="f32", form="var", affin
     return module("jit_layer_norm", [f.text([y], [ty(shape, dt)])])
 
 
+def layer_norm_escape_module(shape=(64, 512), eps=1e-5, dt="f32"):
+    """The "var" LayerNorm with its mean and variance also returned (as
+    [..., 1]): intermediates of the matched pattern that escape it."""
+    shape = list(shape)
+    C = shape[-1]
+    f = Fn("main", [(shape, dt), ([C], dt), ([C], dt)])
+    x = f.arg(0)
+    r = len(shape) - 1
+    mean, kshape = _mean_keepdims(f, x, shape, dt)
+    cen = f.binary("subtract", x, f.bcast(mean, kshape, list(range(r + 1)), shape, dt), shape, dt)
+    var, _ = _mean_keepdims(f, f.binary("multiply", cen, cen, shape, dt), shape, dt)
+    ve = f.binary("add", var, f.splat(eps, kshape, dt), kshape, dt)
+    den = f.bcast(f.unary("sqrt", ve, kshape, dt), kshape, list(range(r + 1)), shape, dt)
+    y = f.binary("divide", cen, den, shape, dt)
+    y = f.binary("multiply", y, f.bcast(f.arg(1), [C], [r], shape, dt), shape, dt)
+    y = f.binary("add", y, f.bcast(f.arg(2), [C], [r], shape, dt), shape, dt)
+    return module("jit_layer_norm_stats", [f.text([y, mean, var], [ty(shape, dt), ty(kshape, dt), ty(kshape, dt)])])
+
+
 def rms_norm_module(shape=(2, 4, 128), eps=1e-6, dt="f32", weight=True, upcast=False):
     shape = list(shape)
     C = shape[-1]
@@ -317,9 +336,10 @@ def _causal_pred(f, T, S):
 
 
 def sdpa_bhtd_module(B=8, H=8, T=128, S=None, D=64, dt="f32", causal=False, scale=None, mask_value=None,
-                     transposed_k=False, inline_softmax=False):
+                     transposed_k=False, inline_softmax=False, return_probs=False):
     """softmax(einsum('bhtd,bhsd->bhts', q, k) * scale [masked]) @ v in BHTD.
-    transposed_k: k passed as [B, H, D, S] and used through a transpose."""
+    transposed_k: k passed as [B, H, D, S] and used through a transpose.
+    return_probs: the softmax probabilities are a second result."""
     S = S or T
     scale = scale if scale is not None else 1.0 / math.sqrt(D)
     kshape = [B, H, D, S] if transposed_k else [B, H, S, D]
@@ -347,9 +367,12 @@ def sdpa_bhtd_module(B=8, H=8, T=128, S=None, D=64, dt="f32", causal=False, scal
     else:
         p = f.call("softmax", [s], [ty(sshape, acc)], ty(sshape, acc))
         funcs.append(softmax_fn(sshape, acc))
+    probs = p
     if dt != acc:
         p = f.convert(p, sshape, acc, dt)
     o, oshape = f.dot_general(p, f.arg(2), sshape, [B, H, S, D], ([0, 1], [0, 1]), ([3], [2]), dt)
+    if return_probs:
+        return module("jit_attention", [f.text([o, probs], [ty(oshape, dt), ty(sshape, acc)])] + funcs)
     return module("jit_attention", [f.text([o], [ty(oshape, dt)])] + funcs)
 
 
@@ -567,6 +590,28 @@ def transformer_module(layers=4, B=32, T=256, d=512, heads=8, mlp=2048, eps=1e-5
         x = f.binary("add", x, m, xs, dt)
     funcs.append(softmax_fn([B, heads, T, T], dt))
     return module("jit_transformer", [f.text([x], [ty(xs, dt)])] + funcs)
+
+
+def config4_inputs(seed=4, layers=4, B=32, T=256, d=512, mlp=2048):
+    """Arguments of transformer_module in order, as BASELINE config 4 states
+    them: x ~ N(0,1), Xavier-uniform weights (U(+-sqrt(6 / (fan_in +
+    fan_out)))), zero biases, LayerNorm scales 1 and offsets 0, drawn from
+    numpy.random.default_rng(seed) in argument order, generated in f32."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+
+    def xavier(fi, fo):
+        a = math.sqrt(6.0 / (fi + fo))
+        return rng.uniform(-a, a, size=(fi, fo)).astype(np.float32)
+
+    ones = lambda n: np.ones(n, np.float32)  # noqa: E731
+    zeros = lambda n: np.zeros(n, np.float32)  # noqa: E731
+    out = [rng.standard_normal((B, T, d), dtype=np.float32)]
+    for _ in range(layers):
+        out += [ones(d), zeros(d), xavier(d, 3 * d), zeros(3 * d), xavier(d, d), zeros(d),
+                ones(d), zeros(d), xavier(d, mlp), zeros(mlp), xavier(mlp, d), zeros(d)]
+    return out
 
 
 def transformer_flops(layers=4, B=32, T=256, d=512, heads=8, mlp=2048):

@@ -231,6 +231,23 @@ def test_sdpa_f32_config2(cuda, nat, oracle, causal):
     check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 0.125, causal=causal), "f32")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_f32_d64_in_place_qkv_slices(cuda, nat, oracle, causal):
+    """Config 4's attention as the plan runs it: q, k and v are BTNH views of
+    one [B*T, 3*512] f32 QKV projection (row stride 1536, element offsets 0,
+    512 and 1024), read in place by flash_f32_d64; B32 T256, 8 heads of 64."""
+    B, T, N, H = 32, 256, 8, 64
+    rng = np.random.default_rng(4)
+    qkv = dev(cuda, rng.standard_normal((B * T, 3 * N * H)), cuda.float32)
+    q, k, v = (qkv[:, j * N * H:(j + 1) * N * H].view(B, T, N, H) for j in range(3))
+    assert q.stride() == (T * 3 * N * H, 3 * N * H, H, 1) and k.storage_offset() == N * H
+    assert nat.sdpa_kernel_name(q, k, v, layout="bthd") == "flash_f32_d64"
+    out = nat.sdpa(q, k, v, scale=H ** -0.5, causal=causal, layout="bthd")
+    t = lambda a: np.ascontiguousarray(host(a).transpose(0, 2, 1, 3))  # noqa: E731
+    ref = oracle.sdpa(t(q), t(k), t(v), H ** -0.5, causal=causal)
+    check_sdpa(out.permute(0, 2, 1, 3), ref, "f32")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("tq,tk,causal", [(100, 77, False), (100, 77, True), (77, 200, True),
@@ -433,6 +450,57 @@ def test_sdpa_decode_mfma_ranges_across_many_lists(cuda, nat, oracle, D):
     assert nat.sdpa_kernel_name(q, k, v, mask=maskd) == "decode_splitkv_mfma"
     out = nat.sdpa(q, k, v, scale=D ** -0.5, mask=maskd)
     check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, mask=mask), "bf16")
+
+
+def select_semantics_ref(oracle, q, k, v, scale, keep):
+    """softmax(where(keep, s, c)) @ v for a very negative finite c, the way
+    jax.nn.dot_product_attention masks: rows with a visible key are the
+    -inf-masked softmax; a row with none has equal scores, so uniform weights
+    and the mean of its kv head's V rows."""
+    B, Hq, Tq, _ = q.shape
+    Hkv, Tk = k.shape[1], k.shape[2]
+    keep = np.broadcast_to(keep, (B, Hq, Tq, Tk))
+    ref = oracle.sdpa(q, k, v, scale, mask=np.where(keep, 0.0, -np.inf))
+    vmean = np.repeat(v.mean(axis=2), Hq // Hkv, axis=1)            # [B, Hq, Dv]
+    full = ~keep.any(-1)                                             # [B, Hq, Tq]
+    ref[full] = np.broadcast_to(vmean[:, :, None, :], ref.shape)[full]
+    return ref
+
+
+@pytest.mark.parametrize("case", ["flash_bf16_d128", "flash_f32_d64", "generic", "decode_splitkv_mfma",
+                                  "decode_splitkv", "decode_splitkv_mfma_shared"])
+@pytest.mark.parametrize("mdt", ["f32", "bf16"])
+def test_sdpa_finite_mask_fully_masked_rows(cuda, nat, oracle, case, mdt):
+    """A mask value of -0.7 * FLT_MAX (JAX's) or bf16's finfo.min on every key
+    of a row returns the mean of V (select semantics), not NaN: the kernels
+    keep log2(e) * mask finite."""
+    shapes = {"flash_bf16_d128": ((2, 4, 64, 128), (2, 2, 300, 128), "bf16"),
+              "flash_f32_d64": ((2, 4, 64, 64), (2, 2, 200, 64), "f32"),
+              "generic": ((2, 4, 33, 40), (2, 2, 90, 40), "f32"),
+              "decode_splitkv_mfma": ((2, 8, 1, 128), (2, 2, 700, 128), "bf16"),
+              "decode_splitkv": ((2, 8, 1, 64), (2, 2, 700, 64), "f32"),
+              "decode_splitkv_mfma_shared": ((2, 8, 1, 128), (2, 2, 700, 128), "bf16")}
+    qs, ks, dt = shapes[case]
+    td = cuda.float32 if dt == "f32" else cuda.bfloat16
+    q, k, v = make_qkv(cuda, 31, qs, ks, td)
+    rng = np.random.default_rng(32)
+    B, Hq, Tq, _ = qs
+    Tk = ks[2]
+    if case.endswith("shared"):
+        keep = np.ones((B, 1, 1, Tk), bool)
+        keep[0, :, :, 400:] = False
+        keep[1] = False                                # batch 1: every key of every row masked
+    else:
+        keep = rng.random((B, Hq, Tq, Tk)) > 0.3
+        keep[0, 1, Tq - 1] = False                     # fully masked rows
+        keep[1, 3, 0] = False
+        keep[1, 2, :, :Tk // 2] = False
+    neg = -0.7 * np.finfo(np.float32).max if mdt == "f32" else float(cuda.finfo(cuda.bfloat16).min)
+    maskd = dev(cuda, np.where(keep, 0.0, neg), cuda.float32).to(cuda.float32 if mdt == "f32" else cuda.bfloat16)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd) == case.replace("_shared", "")
+    out = nat.sdpa(q, k, v, scale=qs[-1] ** -0.5, mask=maskd)
+    assert bool(cuda.isfinite(out.float()).all())
+    check_sdpa(out, select_semantics_ref(oracle, host(q), host(k), host(v), qs[-1] ** -0.5, keep), dt)
 
 
 def test_sdpa_decode_mfma_fully_masked_row_is_nan(cuda, nat):

@@ -2,10 +2,13 @@
 error behaviour without a device, and what Compile's rewriter and planner do
 to each module form (through mfx_pjrt_inspect).
 
-The pattern decisions mirror the reference's RecognizePatterns cases
+The pattern decisions follow the reference's RecognizePatterns cases
 (src/jax_mlx_pjrt.cpp:1857-2044 softmax, :2166-2334 RMSNorm, :2336-2487
-LayerNorm, :2490-2757 SDPA, :8108-8236 custom calls) and its tests of those
-fusions (tests/test_fusion_patterns.py, tests/test_sdpa.py)."""
+LayerNorm, :2490-2757 SDPA, :8108-8236 custom calls).  The reference has no
+tests of these fusions (its tests/ hold test_compilation_coverage.py,
+test_complex.py, test_exhaustive.py and test_exhaustive_while.py, none of
+which covers SDPA, LayerNorm or RMSNorm), so the module texts are this
+repository's own (tests/mlir_modules.py)."""
 import math
 import re
 import subprocess
@@ -315,6 +318,66 @@ def test_custom_calls(api):
     assert n["op"] == "mfx.sdpa_bwd" and n["i:shape"] == [2, 8, 2, 128, 128, 64, 64]
     assert math.isclose(n["f:scale"], 0.3, rel_tol=1e-6)
     assert steps(d) == ["sdpa_bwd"] and d["plan"]["arena_bytes"] > 0  # recomputed O, lse, delta
+
+
+def test_custom_call_sdpa_shape_mismatch(api):
+    """mlx_sdpa checks k and v against q as mlx_sdpa_bwd does: a head size or
+    sequence length that disagrees, or N not a multiple of K, is a compile
+    error rather than a strided read of the wrong elements."""
+    def text(q, k, v):
+        f = M.Fn("main", [(q, "f32"), (k, "f32"), (v, "f32")])
+        o = f.emit(f'stablehlo.custom_call @mlx_sdpa(%arg0, %arg1, %arg2) {{backend_config = "{{}}"}} : '
+                   f'({M.ty(q, "f32")}, {M.ty(k, "f32")}, {M.ty(v, "f32")}) -> {M.ty(q, "f32")}')
+        return M.module("jit_mlx_sdpa", [f.text([o], [M.ty(q, "f32")])])
+
+    q = [2, 64, 4, 64]
+    api.inspect(text(q, [2, 80, 2, 64], [2, 80, 2, 64]))            # GQA, S != T: fine
+    bad = [text(q, [2, 64, 2, 32], [2, 64, 2, 64]),                 # head size
+           text(q, [2, 64, 2, 64], [2, 48, 2, 64]),                 # k / v lengths
+           text(q, [2, 64, 3, 64], [2, 64, 3, 64]),                 # N % K != 0
+           text(q, [1, 64, 2, 64], [1, 64, 2, 64])]                 # batch
+    for t in bad:
+        with pytest.raises(pjrt.PjrtError) as e:
+            api.inspect(t)
+        assert "mlx_sdpa" in e.value.message
+
+
+def test_elementwise_index_width_rule(tmp_path):
+    """The generated elementwise kernels switch to 64-bit loop indices when the
+    grid-stride loop could pass INT32_MAX: work_items - 1 plus one full grid
+    stride (at most 2^20 workgroups of 256 threads)."""
+    src = tmp_path / "t.cpp"
+    src.write_text(r"""
+#include "ew_index.h"
+#include <cstdio>
+#include <initializer_list>
+using namespace mfx;
+int main() {
+  const int64_t stride = kEwMaxBlocks * kEwThreads;           // 2^28
+  const int64_t edge = (int64_t)INT32_MAX + 1 - stride;        // largest int-safe work_items
+  int bad = 0;
+  bad += ew_needs_wide_index(1000);
+  bad += ew_needs_wide_index(edge);
+  bad += !ew_needs_wide_index(edge + 1);
+  bad += !ew_needs_wide_index((1LL << 31) - (1LL << 24));      // the old rule's blind spot
+  bad += !ew_needs_wide_index(1LL << 40);
+  // Brute force on small grids would take hours; check the arithmetic instead:
+  // for every tested size, the last index the loop forms fits an int exactly
+  // when the rule says so.
+  for (int64_t w : {edge - 1, edge, edge + 1, (int64_t)INT32_MAX, (int64_t)1 << 30}) {
+    const int64_t last = (w - 1) + ew_blocks(w) * kEwThreads;
+    bad += (last > INT32_MAX) != ew_needs_wide_index(w);
+  }
+  bad += ew_blocks(0) != 1 || ew_blocks(1) != 1 || ew_blocks(257) != 2 || ew_blocks(1LL << 40) != kEwMaxBlocks;
+  std::printf("%d\n", bad);
+  return bad;
+}
+""")
+    exe = tmp_path / "t"
+    subprocess.run(["g++", "-std=c++17", "-I", str(REPO / "jax-mlx-plugin_amd/csrc/kernels"), str(src), "-o",
+                    str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
 
 
 def test_transformer_plan(api):

@@ -212,6 +212,22 @@ def test_sdpa_predicate_mask(client, oracle):
     assert np.abs(o - ref).max() <= F32_SDPA_TOL
 
 
+def test_sdpa_predicate_mask_fully_masked_row(client, oracle):
+    """select(s > t, scores, -0.7 * FLT_MAX), JAX's mask value, fused as a
+    boolean mask: row 0 sees no key, so all its scores are equal and it
+    returns the mean of V, as the unfused select + softmax does."""
+    rng = np.random.default_rng(9)
+    T = 48
+    q, k, v = (rng.standard_normal((1, 2, T, 64)).astype(np.float32) for _ in range(3))
+    text = M.sdpa_bhtd_module(B=1, H=2, T=T, D=64, causal=True, mask_value=-0.7 * 3.4028234663852886e38)
+    (o,) = run(client, text.replace("GE,", "GT,"), [q, k, v], ["f32"] * 3)
+    keep = np.tril(np.ones((T, T), bool), -1)
+    ref = oracle.sdpa(q, k, v, 0.125, mask=np.where(keep, 0.0, -np.inf)[None, None])
+    ref[:, :, 0] = v.mean(axis=2)
+    assert np.isfinite(o).all()
+    assert np.abs(o - ref).max() <= F32_SDPA_TOL
+
+
 def test_sdpa_finite_mask_through_generic_ops(client, oracle):
     """select(tril, s, -1e9) is not fused: GEMM + select + softmax + GEMM.
     Tolerance: the f32 SDPA bar (rocBLAS f32 GEMMs accumulate in f32)."""
@@ -402,6 +418,53 @@ def test_transformer_block_f32(client, oracle):
     (y,) = run(client, M.transformer_module(layers=layers, B=B, T=T, d=d, heads=heads, mlp=mlp), flat,
                ["f32"] * len(flat))
     assert np.abs(y - transformer_ref(oracle, x, params, heads)).max() <= 2e-4
+
+
+def test_transformer_config4_full_size(client, oracle):
+    """BASELINE config 4 at its own workload: 4 layers, x [32,256,512], d 512,
+    8 heads of 64, MLP 2048, Xavier-uniform weights, zero biases, unit
+    LayerNorm scales, inputs from default_rng(4) -- the module bench.py
+    times, through Client_Compile / Execute.  Its attention is the flash f32
+    kernel reading q/k/v in place from the QKV projection (row stride 1536).
+    Batch elements are independent, so batches 0 and 31 are checked against
+    the fp64 forward.  Bar: the f32 SDPA bar, 1e-4 max-abs (the same network
+    in torch f32 on the CPU is 2.7e-6 from fp64 at ||ref||_inf = 6.8)."""
+    arrays = M.config4_inputs(seed=4)
+    (y,) = run(client, M.transformer_module(), arrays, ["f32"] * len(arrays))
+    assert y.shape == (32, 256, 512) and np.isfinite(y).all()
+    params = [arrays[1 + 12 * i:13 + 12 * i] for i in range(4)]
+    ref = transformer_ref(oracle, arrays[0][[0, 31]], params, 8)
+    err = np.abs(y[[0, 31]] - ref).max()
+    assert err <= F32_SDPA_TOL, err
+
+
+def test_escaping_intermediates_layer_norm(client, oracle):
+    """Escape guard (reference src/jax_mlx_pjrt.cpp:1843-1855): a LayerNorm
+    whose mean and variance are also results.  The fusion fires and the
+    escaping values keep their own ops; all three results are checked."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((64, 512)).astype(np.float32) * 2 + 0.5
+    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    y, mean, var = run(client, M.layer_norm_escape_module((64, 512)), [x, g, b], ["f32"] * 3)
+    x64 = x.astype(np.float64)
+    assert np.abs(y - oracle.layer_norm(x, g, b, 1e-5)).max() <= F32_NORM_TOL
+    assert np.abs(mean[..., 0] - x64.mean(-1)).max() <= F32_NORM_TOL
+    assert np.abs(var[..., 0] - x64.var(-1)).max() <= F32_NORM_TOL * max(1.0, x64.var(-1).max())
+
+
+def test_escaping_intermediates_sdpa_probs(client, oracle):
+    """An attention module that also returns its softmax probabilities: the
+    SDPA fusion still runs for the output, and the escaping probabilities are
+    computed by their own ops.  Both results against the fp64 oracle (the
+    probabilities: softmax of the scaled scores)."""
+    rng = np.random.default_rng(22)
+    B, H, T, D = 2, 2, 64, 64
+    q, k, v = (rng.standard_normal((B, H, T, D)).astype(np.float32) for _ in range(3))
+    o, p = run(client, M.sdpa_bhtd_module(B=B, H=H, T=T, D=D, return_probs=True), [q, k, v], ["f32"] * 3)
+    assert np.abs(o - oracle.sdpa(q, k, v, 0.125)).max() <= F32_SDPA_TOL
+    s = np.einsum("bhtd,bhsd->bhts", q.astype(np.float64), k.astype(np.float64)) * 0.125
+    assert np.abs(p - oracle.softmax(s)).max() <= F32_NORM_TOL
 
 
 # ---------------------------------------------------------------- client API
