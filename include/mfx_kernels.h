@@ -150,8 +150,11 @@ size_t mfx_layer_norm_bwd_workspace_size(const mfx_norm_bwd_args* args);
  *   mask        : optional additive tensor of `mask_dtype`, read at
  *                 b*ms[0] + h*ms[1] + i*ms[2] + j*ms[3] (0 strides
  *                 broadcast); -inf entries remove keys.
- * A query row with every key removed yields NaN (0/0), as the unfused
- * softmax does.
+ * A query row with every key removed by -inf yields NaN (0/0), as the
+ * unfused softmax does.  Finite mask values below -2.3e38 (JAX's
+ * -0.7 * FLT_MAX, finfo.min) are raised to -2.3e38 so that scaling them
+ * stays finite: a row whose keys all carry such a value returns the mean of
+ * V, as jnp.where(mask, s, finite) then softmax does.
  *
  * q_rms_eps >= 0 applies RMSNorm over D to each query row first (rounded to
  * `dtype`, optionally times q_rms_weight[D] of `dtype`), which fuses the
