@@ -200,6 +200,25 @@ int mfx_sdpa_fwd(const mfx_sdpa_args* args, void* stream);
 /* Bytes of workspace mfx_sdpa_fwd needs for these arguments (0 if none). */
 size_t mfx_sdpa_workspace_size(const mfx_sdpa_args* args);
 
+/*
+ * mfx_sdpa_fwd without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: it is
+ * an addition of this library for those callers.
+ *
+ * Same arguments and results as mfx_sdpa_fwd, except that args->workspace is
+ * ignored: the workspace is a static device array of
+ * MFX_SDPA_NOALLOC_SCRATCH_BYTES per device, held until the process ends.
+ * Arguments whose mfx_sdpa_workspace_size() exceeds it are rejected with
+ * MFX_E_WORKSPACE before anything is launched.  The entry point calls no
+ * hipMalloc / hipFree.  Every call on a device shares that device's array, so
+ * calls that overlap on one device (different streams, or host threads
+ * without ordering) race; calls ordered on one stream do not.  The array
+ * keeps the last call's contents; nothing in it needs to start at zero.
+ */
+#define MFX_SDPA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int mfx_sdpa_fwd_noalloc(const mfx_sdpa_args* args, void* stream);
+
 /* Which kernel mfx_sdpa_fwd would launch for these arguments, as a static
  * string ("flash_bf16_d128", "decode_splitkv", ...), or NULL if invalid. */
 const char* mfx_sdpa_kernel_name(const mfx_sdpa_args* args);

@@ -1,8 +1,18 @@
-// mfx_sdpa_fwd: argument validation, kernel selection and workspace layout.
+// mfx_sdpa_fwd: argument validation, kernel selection and workspace layout;
+// mfx_sdpa_fwd_noalloc: the same with the workspace in a static device array.
 #include <cmath>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "sdpa_common.h"
+
+// Workspace of mfx_sdpa_fwd_noalloc (split-KV partials and tile lists, or a
+// normalised copy of q): one copy per device, held until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host it names
+// a stand-in, not the device copy): it uses the per-device address that
+// hipGetSymbolAddress returns.
+static __device__ __align__(256) char scratch[MFX_SDPA_NOALLOC_SCRATCH_BYTES];
 
 namespace mfx {
 namespace {
@@ -112,6 +122,28 @@ const char* kind_name(const Plan& pl) {
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Device address of `scratch` on the current device, looked up once per
+// device (the first mfx_sdpa_fwd_noalloc call there) and kept.
+std::mutex g_scratch_addr_mu;
+std::vector<void*> g_scratch_addr;  // indexed by device ordinal
+
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_addr_mu);
+  if ((size_t)dev >= g_scratch_addr.size()) g_scratch_addr.resize(dev + 1, nullptr);
+  if (!g_scratch_addr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(MFX_E_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_addr[dev] = ptr;
+  }
+  *out = g_scratch_addr[dev];
+  return MFX_OK;
+}
+
 }  // namespace
 }  // namespace mfx
 
@@ -194,6 +226,28 @@ int mfx_sdpa_fwd(const mfx_sdpa_args* args, void* stream) {
     case Kind::kDecodeMfma: return launch_decode_mfma(p, s);
     default: return launch_generic(p, s);
   }
+}
+
+int mfx_sdpa_fwd_noalloc(const mfx_sdpa_args* args, void* stream) {
+  using namespace mfx;
+  Plan pl;
+  int rc = make_plan(args, pl);
+  if (rc != MFX_OK) return rc;
+  const size_t need = align256(pl.partial_bytes) + align256(pl.qnorm_bytes);
+  if (need > MFX_SDPA_NOALLOC_SCRATCH_BYTES)
+    return fail(MFX_E_WORKSPACE, "mfx_sdpa_fwd_noalloc: these arguments need " + std::to_string(need) +
+                                     " bytes of workspace, above the " +
+                                     std::to_string((size_t)MFX_SDPA_NOALLOC_SCRATCH_BYTES) +
+                                     " bytes of its static scratch; call mfx_sdpa_fwd with a workspace");
+  mfx_sdpa_args a = *args;
+  a.workspace = nullptr;
+  a.workspace_bytes = 0;
+  if (need > 0) {
+    rc = noalloc_scratch(&a.workspace);
+    if (rc != MFX_OK) return rc;
+    a.workspace_bytes = MFX_SDPA_NOALLOC_SCRATCH_BYTES;
+  }
+  return mfx_sdpa_fwd(&a, stream);
 }
 
 }  // extern "C"

@@ -163,6 +163,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.mfx_sdpa_bwd_kernel_name.restype = ctypes.c_char_p
     lib.mfx_sdpa_fwd.argtypes = [ctypes.POINTER(SdpaArgs), ctypes.c_void_p]
     lib.mfx_sdpa_fwd.restype = ctypes.c_int
+    lib.mfx_sdpa_fwd_noalloc.argtypes = [ctypes.POINTER(SdpaArgs), ctypes.c_void_p]
+    lib.mfx_sdpa_fwd_noalloc.restype = ctypes.c_int
     lib.mfx_sdpa_workspace_size.argtypes = [ctypes.POINTER(SdpaArgs)]
     lib.mfx_sdpa_workspace_size.restype = ctypes.c_size_t
     lib.mfx_sdpa_kernel_name.argtypes = [ctypes.POINTER(SdpaArgs)]
@@ -374,6 +376,28 @@ def sdpa(q, k, v, *, scale=None, causal=False, mask=None, layout="bhtd", q_rms_e
                   q_rms_eps=q_rms_eps, q_rms_weight=q_rms_weight, workspace=workspace)
     check(load().mfx_sdpa_fwd(ctypes.byref(a), ctypes.c_void_p(_stream_handle(q))))
     return out
+
+
+def sdpa_noalloc(q, k, v, out, *, scale=None, causal=False, mask=None, layout="bhtd", q_rms_eps=None,
+                 q_rms_weight=None):
+    """sdpa() through mfx_sdpa_fwd_noalloc: no device allocation, the
+    workspace is the library's static per-device scratch (at most
+    NOALLOC_SCRATCH_BYTES); the caller passes `out`."""
+    _require_gpu(q, k, v, out, mask, q_rms_weight)
+    a = sdpa_args(q, k, v, out, scale=scale, causal=causal, mask=mask, layout=layout,
+                  q_rms_eps=q_rms_eps, q_rms_weight=q_rms_weight)
+    check(load().mfx_sdpa_fwd_noalloc(ctypes.byref(a), ctypes.c_void_p(_stream_handle(q))))
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # MFX_SDPA_NOALLOC_SCRATCH_BYTES
+
+
+def sdpa_workspace_size(q, k, v, **kw) -> int:
+    """Bytes of workspace mfx_sdpa_fwd needs for these tensors (host-only)."""
+    out = kw.pop("out", None)
+    a = sdpa_args(q, k, v, out if out is not None else q, **kw)
+    return int(load().mfx_sdpa_workspace_size(ctypes.byref(a)))
 
 
 def sdpa_kernel_name(q, k, v, **kw) -> str:
