@@ -1,4 +1,6 @@
-// Flash attention forward, bf16 inputs, fp32 accumulation, gfx950 MFMA.
+// Flash attention forward with an additive mask, bf16 inputs, fp32
+// accumulation, gfx950 MFMA.  (Mask-free calls go to the software-pipelined
+// kernel in sdpa_flash_bf16_pipe.hip.)
 //
 // Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each
 // wavefront owns 32 query rows.  K/V stream through LDS in 64-key tiles, two
@@ -288,9 +290,7 @@ int launch_t(const SdpaParams& p, hipStream_t s) {
 
 template <int D>
 int launch_d(const SdpaParams& p, hipStream_t s) {
-  const bool m = p.mask != nullptr;
-  if (p.causal) return m ? launch_t<D, true, true>(p, s) : launch_t<D, true, false>(p, s);
-  return m ? launch_t<D, false, true>(p, s) : launch_t<D, false, false>(p, s);
+  return p.causal ? launch_t<D, true, true>(p, s) : launch_t<D, false, true>(p, s);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -311,6 +311,9 @@ bool flash_bf16_supports(const SdpaParams& p) {
 }
 
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s) {
+  // Without an additive mask the software-pipelined kernel runs
+  // (sdpa_flash_bf16_pipe.hip); this file's kernel serves masked calls.
+  if (!p.mask) return launch_flash_bf16_pipe(p, s);
   if (p.D == 128) return launch_d<128>(p, s);
   return launch_d<64>(p, s);
 }

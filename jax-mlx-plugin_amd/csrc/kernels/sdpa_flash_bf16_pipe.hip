@@ -1,0 +1,448 @@
+// Flash attention forward without an additive mask (causal or not), bf16
+// inputs, fp32 accumulation, gfx950 MFMA, software-pipelined per wavefront.
+//
+// Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each
+// wavefront owns 32 query rows, held as the B operand of S^T = K Q^T in
+// registers.  K and V tiles of 64 keys stream through two LDS stages each by
+// LDS-DMA (buffer_load ... lds); one vmcnt wait + barrier per tile publishes
+// them.  The products and the operand layouts are those of the masked kernel
+// (sdpa_flash_bf16.hip): S^T = K Q^T and O^T = V^T P^T on
+// v_mfma_f32_32x32x16_bf16, P taken from the S^T accumulator, V^T fragments
+// from transposing LDS reads.
+//
+// The difference is the schedule.  Each wavefront keeps two S tiles in
+// registers and runs, per tile t,
+//   phase A: S(t+1) = K(t+1) Q^T, one MFMA at a time, with the exp2 / bf16 /
+//            row-sum work of S(t) placed between the MFMAs, and
+//   phase B: O^T += V^T(t) P(t)^T, with the row max of S(t+1) placed between
+//            the MFMAs,
+// so the vector work of the softmax runs in the matrix core's shadow instead
+// of between its bursts.  The LDS operand reads are inline asm issued a fixed
+// distance ahead of their MFMAs, each followed by an lgkmcnt wait that counts
+// the reads issued after it (LDS reads complete in order); the compiler
+// therefore adds no waits of its own for the LDS-DMA into the other stage.
+// sched_barrier fences keep this interleave as written.
+//
+// A wavefront's last tile also computes S of the K stage behind it; that S
+// is never used (its max is replaced by -inf), which keeps one code path in
+// the loop and the register allocation spill-free.
+#include <type_traits>
+
+#include "sdpa_tiles.h"
+
+namespace mfx {
+namespace {
+
+constexpr int kBM = 128;  // query rows per workgroup
+constexpr int kBN = 64;   // keys per tile
+constexpr int kNW = 4;    // wavefronts per workgroup
+constexpr int kNT = kNW * 64;
+constexpr int kPfK = 4;   // K operand reads issued ahead of their S MFMA
+constexpr int kPfV = 4;   // V read pairs issued ahead of their PV MFMA
+constexpr int kHeadGroup = 4;  // heads whose q-blocks an XCD issues together
+
+using tiles::kSlack;
+using tiles::s16x4;
+using tiles::tile_swz;
+using tiles::wait_dma;
+
+template <int IMM>
+__device__ __forceinline__ void ds_b128(bf16x8& r, uint32_t a) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ds_tr(s16x4& r, uint32_t a) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(IMM));
+}
+// s_waitcnt lgkmcnt(N) that the named registers depend on, so their uses are
+// not scheduled (or copied) before it.
+template <int N>
+__device__ __forceinline__ void lgkm_tie(bf16x8& r) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_tie(s16x4& a, s16x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+// m = max(m, x, y) without the NaN-quieting copies the compiler adds to fmaxf.
+// Only used far (many MFMAs) after the MFMAs that wrote x and y: the compiler
+// does not add the MFMA -> VALU wait states for inline asm.
+__device__ __forceinline__ void max3(float& m, float x, float y) {
+  asm("v_max3_f32 %0, %0, %1, %2" : "+v"(m) : "v"(x), "v"(y));
+}
+
+// f(integral_constant<int, J>) for J = B .. E-1, in order.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// K / V tile loader: rows [t*kBN, t*kBN + kBN) of one (batch, head) into a
+// swizzled LDS tile.  Instruction i of a wavefront covers rows
+// i*STEP + wave*RPI + lane/DCH of the tile.  Its buffer resource, built once,
+// starts at row i*STEP and ends at the tensor's last row; the tile offset
+// goes into the per-lane offset, which the hardware range-checks, so rows
+// past Tk read as zeros and no address leaves the tensor.
+template <int D>
+struct Loader {
+  static constexpr int DCH = D / 8;
+  static constexpr int RPI = 64 / DCH;
+  static constexpr int LOADS = kBN * DCH / (64 * kNW);
+  static constexpr int STEP = kNW * RPI;
+  static_assert(STEP % tiles::kSwzPeriod<D> == 0 && kBN % tiles::kSwzPeriod<D> == 0, "one offset per lane");
+#if defined(__HIP_DEVICE_COMPILE__)
+  __amdgpu_buffer_rsrc_t rsrc[LOADS];
+#endif
+  uint32_t voff;
+  uint32_t tile_bytes;
+  __device__ __forceinline__ Loader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
+    const int64_t nbytes = (int64_t)Tk * row_stride * 2;
+    tile_bytes = (uint32_t)(kBN * row_stride * 2);
+    const int row = wave * RPI + lane / DCH, slot = lane % DCH;
+    voff = (uint32_t)(((int64_t)row * row_stride + (slot ^ tile_swz<D>(row)) * 8) * 2);
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int64_t off = (int64_t)i * STEP * row_stride * 2;
+      const int64_t rem = nbytes - off;
+      rsrc[i] = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(const_cast<bf16*>(b)) + off, (short)0,
+                                                  rem > 0 ? (int)rem : 0, 0x00020000);
+    }
+#endif
+  }
+  __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t vo = voff + (uint32_t)t * tile_bytes;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[i], (tiles::lds_void_t*)(lds + (kNW * i + wave) * 64 * 8), 16, vo,
+                                               0, 0, 0);
+#endif
+  }
+};
+
+// lgkmcnt of the wait before S MFMA j (MS per tile, reads kPfK ahead) and
+// before PV MFMA j (MP per tile, read pairs kPfV ahead): the reads issued
+// after the one the MFMA needs.
+constexpr int wait_k(int j, int MS) { return kPfK < MS - 1 - j ? kPfK : MS - 1 - j; }
+constexpr int wait_v(int j, int MP) { return 2 * (kPfV < MP - 1 - j ? kPfV : MP - 1 - j); }
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
+  constexpr int TILE = kBN * D;     // elements of one K or V tile
+  constexpr int TB = TILE * 2;      // its bytes
+  constexpr int MS = 2 * (D / 16);  // S MFMAs per tile
+  constexpr int MP = 4 * (D / 32);  // PV MFMAs per tile
+  constexpr int GP = 16 / MS;       // exp pairs per S MFMA
+  constexpr int MH = MP / 2;        // PV MFMAs that carry the max work
+  constexpr int XP = 16 / MH;       // max3 ops per such MFMA
+  static_assert(16 % MS == 0 && 16 % MH == 0, "interleave");
+  __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 K1 V0 V1
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int nmb = (p.Tq + kBM - 1) / kBM;
+  const int BH = p.B * p.Hq;
+  const int id = blockIdx.x;
+  int bh, mblk;
+  if ((BH & 7) == 0) {
+    // Blocks are dealt to the 8 XCDs round-robin.  Each XCD works through
+    // its heads in groups: all q-blocks of a group are issued together,
+    // longest first, so they stream the group's K/V tiles at about the same
+    // time and mostly hit the XCD's L2.
+    const int hg = ((BH >> 3) % kHeadGroup) == 0 ? kHeadGroup : 1;
+    const int xcd = id & 7, slot = id >> 3;
+    const int grp = slot / (hg * nmb), r = slot % (hg * nmb);
+    bh = (grp * hg + r % hg) * 8 + xcd;
+    mblk = nmb - 1 - r / hg;
+  } else {
+    bh = id % BH;
+    mblk = nmb - 1 - id / BH;
+  }
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h / p.group;
+  const bf16* qp = static_cast<const bf16*>(p.q) + b * p.qs[0] + h * p.qs[1];
+  const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+  const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+  bf16* op = static_cast<bf16*>(p.out) + b * p.os[0] + h * p.os[1];
+  const int64_t qs2 = p.qs[2], os2 = p.os[2];
+  const int Tq = p.Tq, Tk = p.Tk;
+
+  const int q0 = mblk * kBM + wave * 32;  // first query row of this wavefront (uniform)
+  const int qi = q0 + l32;
+
+  // Tiles of the workgroup (N) and of this wavefront (nw).
+  int kv_end = Tk;
+  if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kBM));
+  const int N = (kv_end + kBN - 1) / kBN;
+  int nw = 0;
+  if (q0 < Tq) {
+    const int e = CAUSAL ? min(Tk, min(Tq - 1, q0 + 31) + 1) : Tk;
+    nw = (e + kBN - 1) / kBN;
+  }
+  // Tile t needs per-element masking (ragged end, causal diagonal).
+  auto edge = [&](int t) { return (t + 1) * kBN > Tk || (CAUSAL && t * kBN + kBN - 1 > q0); };
+
+  const Loader<D> kload(kp, p.ks[2], Tk, wave, lane), vload(vp, p.vs[2], Tk, wave, lane);
+  bf16* const kst[2] = {smem, smem + TILE};
+  bf16* const vst[2] = {smem + 2 * TILE, smem + 3 * TILE};
+  if (N > 0) {
+    kload.load(0, kst[0], wave);
+    if (N > 1) kload.load(1, kst[1], wave);
+    vload.load(0, vst[0], wave);
+  }
+
+  // Q rows as the B operand (rows past Tq read a valid row and are zeroed).
+  bf16x8 qf[D / 16];
+  {
+    const bf16* qrow = qp + (int64_t)min(qi, Tq - 1) * qs2 + half * 8;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + kk * 16);
+      if (qi >= Tq) raw = u32x4{0u, 0u, 0u, 0u};
+      qf[kk] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  // LDS byte addresses of the operand reads; the stage, the 32-key block of
+  // the K tile and the 16-key step of the V tile are immediate offsets.
+  const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem;
+  uint32_t ka[D / 16];
+  {
+    const int k_sw = tile_swz<D>(l32);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) ka[kk] = base + (uint32_t)((l32 * D + ((kk * 2 + half) ^ k_sw) * 8) * 2);
+  }
+  uint32_t va[D / 32][2];
+  {
+    // Transposing reads: 16 lanes x 4 keys per read; k-slots 0-3 are keys
+    // 4*half + e of the 16-key step, slots 4-7 the same + 8.
+    const int tj = lane & 15, tg = (lane >> 4) & 1;
+    const int v_row = 4 * half + (tj >> 2);
+    const int v_sw = tile_swz<D>(v_row), v_sw8 = tile_swz<D>(v_row + 8);
+    const int v_chunk = tg * 2 + ((tj & 3) >> 1);
+    const int v_sub = (tj & 1) * 4;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      va[dt][0] = base + (uint32_t)((v_row * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw) * 8) * 2);
+      va[dt][1] = base + (uint32_t)(((v_row + 8) * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw8) * 8) * 2);
+    }
+  }
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  // Running exp2 base (log2 units, shared by lanes l and l^32), the lane's
+  // partial row sum, and -base for the exp FMA.
+  float b_run = -INFINITY, l_run = 0.f;
+  float nbase = 0.f;
+  const float sl2 = p.scale_log2;  // > 0 (checked on the host)
+  f32x16 s0[2], s1[2];  // S^T of two tiles: 2 x 32 keys, lane = query
+  u32x4 pb[4];          // P of the current tile: 4 x 16 keys, bf16 pairs
+
+  // Masks S of tile t per element where keys pass Tk or the diagonal.
+  auto mask_tile = [&](f32x16 (&s)[2], int t) {
+    const int kb = t * kBN;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+        if (key >= Tk || (CAUSAL && key > qi)) s[mt][i] = -INFINITY;
+      }
+  };
+  // Row max of S (16 in-lane values + lane l^32) -> lazy base update: the
+  // base only moves when the max passes it by kSlack, and O and l move with it.
+  auto finish_max = [&](float mx) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const float m_l2 = mx * sl2;
+    const bool need = m_l2 > b_run + kSlack;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float nb = need ? m_l2 : b_run;
+      const float alpha = need ? __builtin_amdgcn_exp2f(b_run - nb) : 1.f;
+      b_run = nb;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+    }
+    nbase = b_run == -INFINITY ? 0.f : -b_run;
+  };
+  auto full_max = [&](f32x16 (&s)[2]) -> float {
+    float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const float x = s[g >> 3][(g & 7) * 2], y = s[g >> 3][(g & 7) * 2 + 1];
+      // fmaxf: used right after MFMAs, where the compiler's wait states count.
+      if (g & 1) m1 = fmaxf(m1, fmaxf(x, y));
+      else m0 = fmaxf(m0, fmaxf(x, y));
+    }
+    return fmaxf(m0, m1);
+  };
+  // exp2 of pair g of S into P (bf16) and the row sum of exactly those bf16
+  // values (two per dot2).
+  const bf16x2 one2 = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
+  float lsum0 = 0.f, lsum1 = 0.f;
+  auto exp_pair = [&](f32x16 (&s)[2], int g) {
+    const int mt = g >> 3, i = (g & 7) * 2;
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[mt][i + 1], sl2, nbase));
+    const bf16x2 w = {static_cast<bf16>(p0), static_cast<bf16>(p1)};
+    pb[mt * 2 + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, w);
+    if (g & 1) lsum1 = __builtin_amdgcn_fdot2_f32_bf16(w, one2, lsum1, false);
+    else lsum0 = __builtin_amdgcn_fdot2_f32_bf16(w, one2, lsum0, false);
+  };
+
+  // S of the tile in K stage 0, not interleaved (before the loop).
+  auto s_plain = [&](f32x16 (&s)[2]) {
+    bf16x8 kr[MS];
+#pragma unroll
+    for (int j = 0; j < MS; ++j) {
+      if ((j & 1) == 0) ds_b128<0>(kr[j], ka[j >> 1]);
+      else ds_b128<32 * D * 2>(kr[j], ka[j >> 1]);
+    }
+#pragma unroll
+    for (int j = 0; j < MS; ++j) lgkm_tie<0>(kr[j]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < MS; ++j) s[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], s[j & 1], 0, 0, 0);
+  };
+
+  // One tile (phases A and B above); returns the row max of S_next before
+  // masking.  K stage KS holds tile t+1, V stage VS tile t.
+  auto tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], auto ks_tag, auto vs_tag) -> float {
+    constexpr int KS = decltype(ks_tag)::value;
+    constexpr int VB = (2 + decltype(vs_tag)::value) * TB;
+    bf16x8 kr[MS];
+    s16x4 vr[MP][2];
+    auto rdk = [&](auto j_tag) {  // S MFMA j: 32-key block j & 1, d-slice j >> 1
+      constexpr int j = decltype(j_tag)::value;
+      if constexpr ((j & 1) == 0) ds_b128<KS * TB>(kr[j], ka[j >> 1]);
+      else ds_b128<KS * TB + 32 * D * 2>(kr[j], ka[j >> 1]);
+    };
+    auto rdv = [&](auto j_tag) {  // PV MFMA j: d-block j % (D/32), 16-key step j / (D/32)
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      ds_tr<VB + ks * 16 * D * 2>(vr[j][0], va[dt][0]);
+      ds_tr<VB + ks * 16 * D * 2>(vr[j][1], va[dt][1]);
+    };
+    lsum0 = 0.f;
+    lsum1 = 0.f;
+    static_for<0, kPfK>(rdk);
+    fence();
+    static_for<0, MS>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      if constexpr (j + kPfK < MS) rdk(std::integral_constant<int, j + kPfK>{});
+      lgkm_tie<wait_k(j, MS)>(kr[j]);
+      if constexpr (j < 2)
+        sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], f32x16{}, 0, 0, 0);
+      else
+        sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], sn[j & 1], 0, 0, 0);
+#pragma unroll
+      for (int g = j * GP; g < (j + 1) * GP; ++g) exp_pair(sc, g);
+      fence();
+    });
+    l_run += lsum0 + lsum1;
+    static_for<0, kPfV>(rdv);
+    fence();
+    float m0 = -INFINITY, m1 = -INFINITY;
+    static_for<0, MP>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      if constexpr (j + kPfV < MP) rdv(std::integral_constant<int, j + kPfV>{});
+      lgkm_tie<wait_v(j, MP)>(vr[j][0], vr[j][1]);
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pb[ks]), o[dt], 0, 0, 0);
+      if constexpr (j >= MP - MH) {
+#pragma unroll
+        for (int g = (j - (MP - MH)) * XP; g < (j - (MP - MH) + 1) * XP; ++g) {
+          const float x = sn[g >> 3][(g & 7) * 2], y = sn[g >> 3][(g & 7) * 2 + 1];
+          if (g & 1) max3(m1, x, y);
+          else max3(m0, x, y);
+        }
+      }
+      fence();
+    });
+    return fmaxf(m0, m1);
+  };
+
+  wait_dma();
+  __syncthreads();
+  if (nw > 0) {
+    s_plain(s0);
+    if (edge(0)) mask_tile(s0, 0);
+    finish_max(full_max(s0));
+  }
+  // Iteration t: K(t+1) in K stage (t+1)&1, V(t) in V stage t&1; loads K(t+2)
+  // into K stage t&1 and V(t+1) into V stage (t+1)&1, whose previous tiles
+  // every wavefront has finished reading at the barrier.
+  auto iter = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], auto par_tag) {
+    constexpr int PAR = decltype(par_tag)::value;  // t & 1
+    wait_dma();
+    __syncthreads();
+    if (t + 2 < N) kload.load(t + 2, kst[PAR], wave);
+    if (t + 1 < N) vload.load(t + 1, vst[PAR ^ 1], wave);
+    if (t < nw) {
+      float mx = tile(sc, sn, std::integral_constant<int, PAR ^ 1>{}, std::integral_constant<int, PAR>{});
+      if (t + 1 < nw && edge(t + 1)) {
+        mask_tile(sn, t + 1);
+        mx = full_max(sn);
+      }
+      finish_max(t + 1 < nw ? mx : -INFINITY);
+    }
+  };
+  for (int t = 0; t < N; t += 2) {
+    iter(t, s0, s1, std::integral_constant<int, 0>{});
+    if (t + 1 >= N) break;
+    iter(t + 1, s1, s0, std::integral_constant<int, 1>{});
+  }
+
+  const float lt = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / lt;
+  if (p.lse && half == 0 && qi < Tq) p.lse[(int64_t)bh * Tq + qi] = b_run + __log2f(lt);
+  if (qi < Tq) {
+    bf16* orow = op + qi * os2;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(o[dt][g * 4 + e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
+      }
+  }
+}
+
+template <int D, bool CAUSAL>
+int launch_t(const SdpaParams& p, hipStream_t s) {
+  const int nmb = (p.Tq + kBM - 1) / kBM;
+  const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
+  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, CAUSAL>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
+  return launch_status("flash_bf16_pipe_kernel");
+}
+
+}  // namespace
+
+// Mask-free flash attention (the caller checked flash_bf16_supports).
+int launch_flash_bf16_pipe(const SdpaParams& p, hipStream_t s) {
+  if (p.D == 128) return p.causal ? launch_t<128, true>(p, s) : launch_t<128, false>(p, s);
+  return p.causal ? launch_t<64, true>(p, s) : launch_t<64, false>(p, s);
+}
+
+}  // namespace mfx
