@@ -128,6 +128,10 @@ struct ParseError : std::runtime_error {
 // "op"(...) form for the ops the planner knows).  Throws ParseError.
 Module parse_module(const std::string& text);
 
+// Structural checks (operand/result shapes against each op's attributes);
+// throws ParseError on the first violation.
+void verify_module(const Module& m);
+
 // Replaces every func.call by the callee's body (recursively), so fused
 // patterns are matched across jax.nn helper boundaries such as @softmax.
 void inline_calls(Module& m);

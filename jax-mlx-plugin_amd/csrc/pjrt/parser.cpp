@@ -977,6 +977,7 @@ class Parser {
       classify_reducer(node);
       if (!node.strs.count("reduce")) fail("reduce without a recognisable reducer");
     }
+    if (node.op == "stablehlo.concatenate") take("dimension", "dimension");
   }
 
   void set_literal(Node& node, const std::string& text, const Type& t) {
@@ -1125,6 +1126,8 @@ class Parser {
     ws();
     if (peek() == '{') attr_dict(node);
     signature(ins, outs);
+    // concatenate's pretty form spells its axis "dim".
+    if (op == "stablehlo.concatenate" && node.ints.count("dim")) node.ints["dimension"] = node.ints["dim"];
   }
 };
 

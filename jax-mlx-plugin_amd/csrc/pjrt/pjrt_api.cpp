@@ -376,6 +376,7 @@ struct Compiled {
 
 Compiled compile_text(const std::string& text) {
   Module m = parse_module(text);
+  verify_module(m);
   inline_calls(m);
   Compiled c;
   c.module_name = m.name;

@@ -8,6 +8,7 @@ benchmark).  Argument structs mirror include/pjrt_abi.h field for field.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, Structure, c_bool, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
@@ -152,7 +153,8 @@ class Api:
     _HEADER = 40  # struct_size, extension_start, PJRT_Api_Version (24 bytes)
 
     def __init__(self, path: str | Path | None = None):
-        p = Path(path) if path else PLUGIN_LIB
+        # MFX_PJRT_LIB selects another build of the plugin (the tests' sanitizer build).
+        p = Path(path) if path else Path(os.environ.get("MFX_PJRT_LIB", PLUGIN_LIB))
         if not p.exists():
             raise FileNotFoundError(f"{p} is not built; run jax-mlx-plugin_amd/build.py")
         self.lib = ctypes.CDLL(str(p))

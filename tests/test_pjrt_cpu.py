@@ -380,6 +380,25 @@ int main() {
     assert r.returncode == 0, r.stdout
 
 
+def test_structurally_invalid_modules_are_rejected(api):
+    """Regression cases the sanitizer fuzz found (each used to read out of
+    bounds in the rewriter or planner): the verifier rejects them with
+    INVALID_ARGUMENT before either runs."""
+    ln = M.layer_norm_module(shape=(4, 64, 128))
+    # broadcast_in_dim whose dims list is shorter than the operand rank
+    bad_bcast = ln.replace("dims = [0, 1]", "dims = [0]", 1)
+    # a softmax body returning a value of another type than its signature
+    dpa = M.dot_product_attention_module(B=1, T=64, N=4, H=64)
+    bad_return = dpa.replace("return %13 : tensor<1x4x1x64x64xf32>", "return %1 : tensor<1x4x1x64x64xf32>")
+    # a binary op with one operand
+    bad_arity = dpa.replace("stablehlo.subtract %arg0, %6 :", "stablehlo.subtract %arg0:")
+    for text, what in ((bad_bcast, "broadcast"), (bad_return, "func.call"), (bad_arity, "subtract")):
+        assert text not in (ln, dpa), what
+        with pytest.raises(pjrt.PjrtError) as e:
+            api.inspect(text)
+        assert e.value.code_name == "INVALID_ARGUMENT" and what in e.value.message, e.value.message
+
+
 def test_transformer_plan(api):
     d = api.inspect(M.transformer_module(layers=2, B=2, T=64, d=128, heads=4, mlp=256))
     ops = [n["op"] for n in fused(d)]
