@@ -64,6 +64,35 @@ def time_launches(torch, fn, steps: int, warmup: int):
     return total / steps, per[len(per) // 2], total
 
 
+def graph_replay_us(torch, fn, reps: int = 100):
+    """Device time per call of fn() replayed from a captured graph (`reps`
+    calls per graph, 5 replays): the launch rate without the host's per-call
+    cost (Python argument marshalling and the launch itself).  None when
+    capture is unavailable."""
+    try:
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.current_stream().wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (5 * reps)
+    except Exception as exc:  # graph capture unavailable: report the per-call figure only
+        log(f"  graph replay skipped: {exc}")
+        return None
+
+
 def profiled_traffic(name):
     """HBM bytes per launch of the profiled kernel: FETCH_SIZE + WRITE_SIZE
     from rocprofv3 counter runs, calibrated against a plain device copy, as
@@ -203,31 +232,7 @@ def bench_config1(torch, native, steps, warmup):
     y = torch.empty_like(x)
     avg_ms, med_ms, _ = time_launches(torch, lambda: native.layer_norm(x, g, b, 1e-5, out=y), steps, warmup)
     nbytes = 4198400.0
-    # The same launch replayed from a captured graph (100 launches per
-    # replay): the device time without the host's per-call launch cost.
-    graph_us = None
-    try:
-        reps = 100
-        stream = torch.cuda.Stream()
-        stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
-            native.layer_norm(x, g, b, 1e-5, out=y)
-        torch.cuda.current_stream().wait_stream(stream)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(reps):
-                native.layer_norm(x, g, b, 1e-5, out=y)
-        graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(5):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        graph_us = e0.elapsed_time(e1) * 1e3 / (5 * reps)
-    except Exception as exc:  # graph capture unavailable: report the per-call figure only
-        log(f"  graph replay skipped: {exc}")
+    graph_us = graph_replay_us(torch, lambda: native.layer_norm(x, g, b, 1e-5, out=y))
     res = {"shape": [8, 128, 512], "avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "bytes": nbytes,
            "GBps": nbytes / (avg_ms * 1e-3) / 1e9,
            "note": "4.2 MB per call: below launch latency and inside the 256 MB Infinity Cache"}
@@ -247,10 +252,17 @@ def bench_config2(torch, native, steps, warmup):
     avg_ms, med_ms, _ = time_launches(torch, lambda: native.sdpa(q, k, v, scale=0.125, out=out), steps,
                                       warmup)
     flops = 4.0 * 8 * 8 * 128 * 128 * 64
-    return {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "flops": flops,
-            "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
-            "frac_fp32_peak": flops / (avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
-            "kernel": native.sdpa_kernel_name(q, k, v)}
+    res = {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "flops": flops,
+           "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
+           "frac_fp32_peak": flops / (avg_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+           "kernel": native.sdpa_kernel_name(q, k, v),
+           "note": "avg_us is the eager per-call rate through the Python ctypes wrapper, host-bound at this size"}
+    graph_us = graph_replay_us(torch, lambda: native.sdpa(q, k, v, scale=0.125, out=out))
+    if graph_us:
+        res["graph_replay_us"] = graph_us
+        res["graph_TFLOPs"] = flops / (graph_us * 1e-6) / 1e12
+        res["graph_frac_fp32_peak"] = res["graph_TFLOPs"] / PEAK_FP32_TFLOPS
+    return res
 
 
 def bench_config5(torch, native, steps, warmup, rotate=2):

@@ -62,8 +62,16 @@ def _run(cmd: list[str]) -> None:
         print("\n".join(lines), file=sys.stderr)
 
 
+# Per-file code-generation options.  sdpa_flash_f32.hip: MFMA accumulators in
+# VGPRs rather than AGPRs (its kernels read every accumulator back into VALU
+# work -- softmax, rescale, merge -- and the AGPR form adds a move per read).
+HIP_FILE_FLAGS = {
+    "sdpa_flash_f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile_hip(src: Path, obj: Path) -> Path:
-    _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+    _run([HIPCC, *HIP_FLAGS, *HIP_FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)])
     return obj
 
 

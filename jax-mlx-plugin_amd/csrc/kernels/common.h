@@ -43,6 +43,10 @@ inline int dtype_size(int dt) {
 // failure.
 void* device_scratch(size_t bytes);
 
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int device_cu_count();
+
 // ---- device helpers ---------------------------------------------------------
 
 typedef __bf16 bf16;

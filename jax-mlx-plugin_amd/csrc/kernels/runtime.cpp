@@ -66,6 +66,27 @@ void* device_scratch(size_t bytes) {
   return s.ptr;
 }
 
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> counts;  // indexed by device ordinal, 0 = not queried
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if ((size_t)dev >= counts.size()) counts.resize(dev + 1, 0);
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
+
 }  // namespace mfx
 
 extern "C" {

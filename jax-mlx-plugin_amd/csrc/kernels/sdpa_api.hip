@@ -113,7 +113,9 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
 const char* kind_name(const Plan& pl) {
   switch (pl.kind) {
     case Kind::kFlashBf16: return pl.p.D == 128 ? "flash_bf16_d128" : "flash_bf16_d64";
-    case Kind::kFlashF32: return pl.p.D == 128 ? "flash_f32_d128" : "flash_f32_d64";
+    case Kind::kFlashF32:
+      if (flash_f32_use_split(pl.p)) return pl.p.D == 128 ? "flash_f32_split_d128" : "flash_f32_split_d64";
+      return pl.p.D == 128 ? "flash_f32_d128" : "flash_f32_d64";
     case Kind::kDecode: return "decode_splitkv";
     case Kind::kDecodeMfma: return "decode_splitkv_mfma";
     default: return "generic";

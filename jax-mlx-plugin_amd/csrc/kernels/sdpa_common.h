@@ -76,6 +76,7 @@ int launch_generic(const SdpaParams& p, hipStream_t s);
 
 bool flash_bf16_supports(const SdpaParams& p);
 bool flash_f32_supports(const SdpaParams& p);
+bool flash_f32_use_split(const SdpaParams& p);  // the key-split variant runs
 bool decode_supports(const SdpaParams& p);
 bool decode_mfma_supports(const SdpaParams& p);
 int decode_mfma_tile();  // keys per tile of the MFMA decode

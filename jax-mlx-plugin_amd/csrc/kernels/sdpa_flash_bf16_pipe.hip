@@ -100,11 +100,11 @@ struct Loader {
   uint32_t voff;
   uint32_t tile_bytes;
   __device__ __forceinline__ Loader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
-    const int64_t nbytes = (int64_t)Tk * row_stride * 2;
     tile_bytes = (uint32_t)(kBN * row_stride * 2);
     const int row = wave * RPI + lane / DCH, slot = lane % DCH;
     voff = (uint32_t)(((int64_t)row * row_stride + (slot ^ tile_swz<D>(row)) * 8) * 2);
 #if defined(__HIP_DEVICE_COMPILE__)
+    const int64_t nbytes = (int64_t)Tk * row_stride * 2;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int64_t off = (int64_t)i * STEP * row_stride * 2;

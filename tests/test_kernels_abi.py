@@ -43,8 +43,12 @@ def test_kernel_selection_per_config(native):
     # config 3: causal bf16 B4/H32/T2048/d128 -> bf16 MFMA flash kernel
     q, k, v = _cpu_tensors(torch, (4, 32, 2048, 128), (4, 32, 2048, 128), (4, 32, 2048, 128))
     assert native.sdpa_kernel_name(q, k, v, causal=True) == "flash_bf16_d128"
-    # config 2: f32 B8/H8/T128/d64 -> fp32 MFMA flash kernel
+    # config 2: f32 B8/H8/T128/d64 -> fp32 MFMA flash kernel, key-split variant (64 workgroups of
+    # 128 rows would leave most CUs idle)
     q, k, v = _cpu_tensors(torch, (8, 8, 128, 64), (8, 8, 128, 64), (8, 8, 128, 64), dtype=torch.float32)
+    assert native.sdpa_kernel_name(q, k, v) == "flash_f32_split_d64"
+    # config 4's attention (B32, 8 heads, T256): 512 workgroups -> the 128-row kernel
+    q, k, v = _cpu_tensors(torch, (32, 8, 256, 64), (32, 8, 256, 64), (32, 8, 256, 64), dtype=torch.float32)
     assert native.sdpa_kernel_name(q, k, v) == "flash_f32_d64"
     # config 5: GQA decode Hq32/Hkv8, Tq=1 -> split-KV decode on the matrix cores
     q, k, v = _cpu_tensors(torch, (16, 32, 1, 128), (16, 8, 8192, 128), (16, 8, 8192, 128))

@@ -226,7 +226,7 @@ def check_sdpa(out, ref, dtype):
 @pytest.mark.parametrize("causal", [False, True])
 def test_sdpa_f32_config2(cuda, nat, oracle, causal):
     q, k, v = make_qkv(cuda, 2, (8, 8, 128, 64), (8, 8, 128, 64), cuda.float32)
-    assert nat.sdpa_kernel_name(q, k, v) == "flash_f32_d64"
+    assert nat.sdpa_kernel_name(q, k, v) == "flash_f32_split_d64"
     out = nat.sdpa(q, k, v, scale=0.125, causal=causal)
     check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 0.125, causal=causal), "f32")
 
@@ -246,6 +246,27 @@ def test_sdpa_f32_d64_in_place_qkv_slices(cuda, nat, oracle, causal):
     t = lambda a: np.ascontiguousarray(host(a).transpose(0, 2, 1, 3))  # noqa: E731
     ref = oracle.sdpa(t(q), t(k), t(v), H ** -0.5, causal=causal)
     check_sdpa(out.permute(0, 2, 1, 3), ref, "f32")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("tq,tk,hq,hkv,causal,masked", [(128, 128, 8, 8, False, False), (100, 77, 4, 2, True, False),
+                                                        (33, 300, 4, 1, False, True), (77, 200, 2, 2, True, True),
+                                                        (5, 1000, 4, 4, False, False), (31, 31, 4, 2, True, False)])
+def test_sdpa_f32_key_split(cuda, nat, oracle, D, tq, tk, hq, hkv, causal, masked):
+    """The key-split f32 kernel (four wavefronts per 32 query rows, partials
+    merged through LDS): ragged lengths, GQA, causal and an additive mask
+    with -inf holes, against the fp64 oracle."""
+    q, k, v = make_qkv(cuda, 15, (2, hq, tq, D), (2, hkv, tk, D), cuda.float32)
+    mask = None
+    if masked:
+        m = np.random.default_rng(16).standard_normal((2, 1, tq, tk)) * 0.5
+        m[..., ::5] = -np.inf
+        m[..., 0] = 0.0
+        mask = m
+    maskd = None if mask is None else dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, causal=causal, mask=maskd) == f"flash_f32_split_d{D}"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, causal=causal, mask=maskd)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=causal, mask=mask), "f32")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -467,7 +488,9 @@ def select_semantics_ref(oracle, q, k, v, scale, keep):
     return ref
 
 
-@pytest.mark.parametrize("case", ["flash_bf16_d128", "flash_f32_d64", "generic", "decode_splitkv_mfma",
+@pytest.mark.parametrize("case", ["flash_bf16_d128", "flash_f32_split_d64", "flash_f32_split_d128", "flash_f32_d64",
+                                  "flash_f32_d128", "generic",
+                                  "decode_splitkv_mfma",
                                   "decode_splitkv", "decode_splitkv_mfma_shared"])
 @pytest.mark.parametrize("mdt", ["f32", "bf16"])
 def test_sdpa_finite_mask_fully_masked_rows(cuda, nat, oracle, case, mdt):
@@ -475,7 +498,10 @@ def test_sdpa_finite_mask_fully_masked_rows(cuda, nat, oracle, case, mdt):
     of a row returns the mean of V (select semantics), not NaN: the kernels
     keep log2(e) * mask finite."""
     shapes = {"flash_bf16_d128": ((2, 4, 64, 128), (2, 2, 300, 128), "bf16"),
-              "flash_f32_d64": ((2, 4, 64, 64), (2, 2, 200, 64), "f32"),
+              "flash_f32_split_d64": ((2, 4, 64, 64), (2, 2, 200, 64), "f32"),
+              "flash_f32_split_d128": ((2, 4, 64, 128), (2, 2, 200, 128), "f32"),
+              "flash_f32_d64": ((16, 32, 128, 64), (16, 16, 200, 64), "f32"),  # 512 workgroups
+              "flash_f32_d128": ((16, 32, 128, 128), (16, 16, 200, 128), "f32"),
               "generic": ((2, 4, 33, 40), (2, 2, 90, 40), "f32"),
               "decode_splitkv_mfma": ((2, 8, 1, 128), (2, 2, 700, 128), "bf16"),
               "decode_splitkv": ((2, 8, 1, 64), (2, 2, 700, 64), "f32"),
