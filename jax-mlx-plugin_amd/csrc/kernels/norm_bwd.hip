@@ -8,8 +8,9 @@
 //   dgamma = sum_rows(dy * xhat),  dbeta = sum_rows(dy)
 //
 // Pass 1 (ln_bwd_rows): a row is owned by 16 / 64 lanes of a wavefront or by
-// a 256-thread workgroup, as in the forward kernel.  x and dy are read once
-// into registers as 16-byte vectors; mean and variance are recomputed from x
+// a 256-thread workgroup, as in the forward kernel; 16- and 64-lane groups
+// take rows in pairs with both rows' loads in flight together.  x and dy are
+// read once into registers as 16-byte vectors; mean and variance are recomputed from x
 // (two passes over registers), dx is written once.  Each lane keeps running
 // dgamma / dbeta sums for the columns it owns across every row its group
 // visits, and the workgroup folds its groups into one fp32 partial row pair
@@ -57,16 +58,19 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
 #pragma unroll
     for (int j = 0; j < VEC; ++j) ag[i][j] = ab[i][j] = 0.f;
 
-  // With LANES == 256 the whole workgroup owns one row and the reductions
-  // synchronise through LDS, so the loop bound is uniform per workgroup.
-  for (int64_t row = (int64_t)blockIdx.x * RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+  // With 16 or 64 lanes per row, rows come in pairs (row, row + stride): both
+  // rows' x and dy loads are issued before either row's reductions, so a
+  // wavefront keeps two rows of reads in flight.  With LANES == 256 the
+  // whole workgroup owns each row and the reductions synchronise through
+  // LDS, so the loop bound is uniform per workgroup.
+  const int64_t stride = (int64_t)gridDim.x * RPB;
+  auto load_row = [&](int64_t row, bool valid, float (&xv)[NV][VEC], float (&g)[NV][VEC]) {
     const V* xr = reinterpret_cast<const V*>(x + row * xs);
     const V* gr = reinterpret_cast<const V*>(dy + row * gs);
-    float xv[NV][VEC], g[NV][VEC];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int vi = i * LANES + lane;
-      if (vi < nvec) {
+      if (valid && vi < nvec) {
         unpack16<T>(xr[vi], xv[i]);
         unpack16<T>(gr[vi], g[i]);
       } else {
@@ -74,6 +78,8 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
         for (int j = 0; j < VEC; ++j) xv[i][j] = g[i][j] = 0.f;
       }
     }
+  };
+  auto finish_row = [&](int64_t row, bool valid, float (&xv)[NV][VEC], float (&g)[NV][VEC]) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
     for (int i = 0; i < NV; ++i)
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        xv[i][j] *= inv;  // xhat
+        xv[i][j] *= inv;  // xhat (0 for an absent row, whose dy is 0 too)
         const float d = g[i][j] * gv[i][j];
         s1 += d;
         s2 += d * xv[i][j];
@@ -105,6 +111,7 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
       }
     const float m1 = row_reduce<LANES, false>(s1, lds) * inv_n;
     const float m2 = row_reduce<LANES, false>(s2, lds) * inv_n;
+    if (!valid) return;
     V* dr = reinterpret_cast<V*>(dx + row * dxs);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -114,6 +121,76 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
 #pragma unroll
       for (int j = 0; j < VEC; ++j) o[j] = inv * (g[i][j] * gv[i][j] - m1 - xv[i][j] * m2);
       dr[vi] = pack16<T>(o);
+    }
+  };
+  if constexpr (LANES <= 64) {
+    for (int64_t row = (int64_t)blockIdx.x * RPB + grp; row < rows; row += 2 * stride) {
+      const bool second = row + stride < rows;
+      float xa[NV][VEC], ga[NV][VEC], xb[NV][VEC], gb[NV][VEC];
+      load_row(row, true, xa, ga);
+      load_row(row + stride, second, xb, gb);
+      finish_row(row, true, xa, ga);
+      finish_row(row + stride, second, xb, gb);
+    }
+  } else {
+    // A 256-lane row already has 256 x NV 16-byte loads in flight, and a
+    // second row's registers would cost occupancy.
+    for (int64_t row = blockIdx.x; row < rows; row += stride) {
+      const V* xr = reinterpret_cast<const V*>(x + row * xs);
+      const V* gr = reinterpret_cast<const V*>(dy + row * gs);
+      float xv[NV][VEC], g[NV][VEC];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int vi = i * LANES + lane;
+        if (vi < nvec) {
+          unpack16<T>(xr[vi], xv[i]);
+          unpack16<T>(gr[vi], g[i]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) xv[i][j] = g[i][j] = 0.f;
+        }
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) s += xv[i][j];
+      const float mean = row_reduce<LANES, false>(s, lds) * inv_n;
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const bool in = (i * LANES + lane) < nvec;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          xv[i][j] = in ? xv[i][j] - mean : 0.f;
+          q += xv[i][j] * xv[i][j];
+        }
+      }
+      const float inv = rsqrtf(row_reduce<LANES, false>(q, lds) * inv_n + eps);
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          xv[i][j] *= inv;  // xhat
+          const float d = g[i][j] * gv[i][j];
+          s1 += d;
+          s2 += d * xv[i][j];
+          ag[i][j] = fmaf(g[i][j], xv[i][j], ag[i][j]);
+          ab[i][j] += g[i][j];
+        }
+      const float m1 = row_reduce<LANES, false>(s1, lds) * inv_n;
+      const float m2 = row_reduce<LANES, false>(s2, lds) * inv_n;
+      V* dr = reinterpret_cast<V*>(dx + row * dxs);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int vi = i * LANES + lane;
+        if (vi >= nvec) continue;
+        float o[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) o[j] = inv * (g[i][j] * gv[i][j] - m1 - xv[i][j] * m2);
+        dr[vi] = pack16<T>(o);
+      }
     }
   }
 
