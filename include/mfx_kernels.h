@@ -433,7 +433,10 @@ int mfx_reduce(const mfx_reduce_args* args, void* stream);
  *   C_i[m,n] = sum_k op(A_i)[m,k] * op(B_i)[k,n]
  * with A_i at a + i*stride_a stored [m][k] (lda) or, if trans_a, [k][m];
  * B_i at b + i*stride_b stored [k][n] (ldb) or, if trans_b, [n][k].
- * fp32 accumulation; a/b share `dtype`, c has `c_dtype`.
+ * fp32 accumulation; a/b share `dtype`, c has `c_dtype`.  f32 products
+ * without transposes whose A and B rows are 16-byte aligned (k % 4 == 0,
+ * lda and ldb multiples of 4, even n) run on the hand-written MFMA tile
+ * kernel; every other case on rocBLAS (mfx_gemm_kernel_name tells which).
  * Replaces the dot_general lowering (reference src/jax_mlx_pjrt.cpp:4577-4666). */
 typedef struct {
   const void* a;
@@ -449,6 +452,43 @@ typedef struct {
 } mfx_gemm_args;
 
 int mfx_gemm(const mfx_gemm_args* args, void* stream);
+
+/* Name of the kernel mfx_gemm runs for args (no device needed; pointers are
+ * read for their alignment): "gemm_f32_tile" (hand-written MFMA kernel) or
+ * "rocblas".  For tests and traces. */
+const char* mfx_gemm_kernel_name(const mfx_gemm_args* args);
+
+/* GEMM with a fused elementwise epilogue: out = epi(inputs) where epi's
+ * input `c_input` is the GEMM result C = A B, read at the program's output
+ * index (contiguous strides, fp32; its data pointer and gemm->c are
+ * ignored): C is never stored.  The program's output index space must be C's
+ * [batch * m, n] (rank-1..8 dims whose trailing dims span exactly n) with a
+ * contiguous output aligned to two elements; gemm must be an f32 row-major
+ * product the tile kernel handles (no transposes, k % 4 == 0, even n, lda and
+ * ldb multiples of 4 -- so n % 4 == 0 for a contiguous B -- A and B 16-byte
+ * aligned, ldc = n, stride_c = m * n).  The kernel is generated from the program and compiled
+ * with hipRTC for gfx950 on first use (cached per device and program); the
+ * arithmetic is that of mfx_elementwise, so the result equals mfx_gemm
+ * followed by mfx_elementwise bit for bit.  Returns MFX_E_UNSUPPORTED for
+ * pairs it cannot fuse (run the two calls instead).
+ * Replaces the MLX matmul + fused elementwise kernels that mx::compile
+ * produces for a dot_general and its consumers (reference
+ * src/jax_mlx_pjrt.cpp:4577-4666 and 9063-9081). */
+int mfx_gemm_ew(const mfx_gemm_args* gemm, const mfx_ew_program* epi, int c_input, void* stream);
+
+/* Host-only check (no device needed) that mfx_gemm_ew accepts the pair; the
+ * pointers are read for their alignment only. */
+int mfx_gemm_ew_check(const mfx_gemm_args* gemm, const mfx_ew_program* epi, int c_input);
+
+/* Compiles the fused kernel ahead of its first mfx_gemm_ew call (needs a
+ * current device). */
+int mfx_gemm_ew_prepare(const mfx_gemm_args* gemm, const mfx_ew_program* epi, int c_input);
+
+/* Diagnostic: writes the generated source of the fused kernel (which
+ * includes "gemm_f32_tile.h") into buf (NUL-terminated, truncated to
+ * size) and returns its full length, or -1 when the pair cannot be fused. */
+int64_t mfx_gemm_ew_source(const mfx_gemm_args* gemm, const mfx_ew_program* epi, int c_input, char* buf,
+                           int64_t size);
 
 #ifdef __cplusplus
 }

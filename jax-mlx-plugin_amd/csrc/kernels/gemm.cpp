@@ -1,14 +1,17 @@
-// mfx_gemm: batched strided GEMM for the unfused dot_general ops.
+// mfx_gemm: batched strided GEMM for the dot_general ops.
 //
-// A plain library GEMM (no fused epilogue), so it goes to rocBLAS's
-// gemm_strided_batched_ex with fp32 accumulation.  Row-major C = op(A) op(B)
-// is issued as the column-major product C^T = op(B)^T op(A)^T.
+// f32 row-major products without transposes (the dense layers of a
+// transformer) run on the hand-written MFMA tile kernel (gemm_f32.hip);
+// every other case goes to rocBLAS's gemm_strided_batched_ex with fp32
+// accumulation, issuing row-major C = op(A) op(B) as the column-major
+// product C^T = op(B)^T op(A)^T.
 #include <rocblas/rocblas.h>
 
 #include <mutex>
 #include <vector>
 
 #include "common.h"
+#include "gemm_f32.h"
 
 namespace mfx {
 namespace {
@@ -59,6 +62,7 @@ extern "C" int mfx_gemm(const mfx_gemm_args* a, void* stream) {
   const int64_t b_cols = a->trans_b ? a->k : a->n;
   if (a->lda < a_cols || a->ldb < b_cols || a->ldc < a->n)
     return fail(MFX_E_INVALID, "gemm leading dimension too small");
+  if (gemm_f32_supported(*a)) return gemm_f32_launch(*a, static_cast<hipStream_t>(stream));
   rocblas_handle h;
   int rc = handle_for_current_device(&h);
   if (rc != MFX_OK) return rc;
@@ -83,4 +87,9 @@ extern "C" int mfx_gemm(const mfx_gemm_args* a, void* stream) {
   if (st != rocblas_status_success)
     return fail(MFX_E_HIP, std::string("rocblas_gemm_strided_batched_ex: ") + rocblas_status_to_string(st));
   return MFX_OK;
+}
+
+extern "C" const char* mfx_gemm_kernel_name(const mfx_gemm_args* a) {
+  if (!a) return "invalid";
+  return mfx::gemm_f32_supported(*a) ? "gemm_f32_tile" : "rocblas";
 }

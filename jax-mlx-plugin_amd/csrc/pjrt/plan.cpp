@@ -184,6 +184,20 @@ class Planner {
     std::vector<int> reads, writes;
   };
   std::vector<StepIO> io_;
+  // Launch arguments of GEMM and elementwise steps (by step index), for the
+  // pass that fuses an elementwise program into the GEMM it consumes.
+  struct GemmMeta {
+    mfx_gemm_args g;
+    int64_t aoff, boff;  // byte offsets into the A / B values
+    int av, bv, out_v;
+  };
+  struct EwMeta {
+    mfx_ew_program prog;
+    std::vector<ProgIn> ins;
+    int out_value;
+  };
+  std::map<size_t, GemmMeta> gemm_meta_;
+  std::map<size_t, EwMeta> ew_meta_;
   std::vector<Type> temp_types_;
   std::vector<int64_t> temp_bytes_;
   std::shared_ptr<std::vector<Loc>> loc_ = std::make_shared<std::vector<Loc>>();
@@ -588,6 +602,7 @@ class Planner {
     s.bytes = (double)t.bytes();
     auto loc = loc_;
     Plan* plan = &plan_;
+    ew_meta_[plan_.steps_.size()] = EwMeta{prog, ins, out_value};
     s.run = [prog, ins, out_value, loc, plan](const ExecBuffers& b, std::string& err) {
       mfx_ew_program p = prog;
       p.out = plan->ptr((*loc)[out_value], b);
@@ -781,6 +796,7 @@ class Planner {
     s.label = "dot_general " + std::to_string(batch) + "x" + std::to_string(M) + "x" + std::to_string(N) + "x" +
               std::to_string(K);
     s.flops = 2.0 * batch * M * N * K;
+    gemm_meta_[plan_.steps_.size()] = GemmMeta{g, aoff, boff, av, bv, out_v};
     s.run = [g, aoff, boff, av, bv, out_v, loc, plan](const ExecBuffers& b, std::string& err) {
       mfx_gemm_args a = g;
       a.a = (char*)plan->ptr((*loc)[av], b) + aoff;
@@ -1253,6 +1269,8 @@ class Planner {
   void emit_all() {
     plan_.steps_.clear();
     io_.clear();
+    gemm_meta_.clear();
+    ew_meta_.clear();
     temp_types_.clear();
     temp_bytes_.clear();
     flat_alias_.clear();
@@ -1298,6 +1316,110 @@ class Planner {
       }
       seen.insert(v);
     }
+    fuse_gemm_epilogues();
+  }
+
+  // A GEMM step followed by an elementwise step that is the only reader of
+  // the GEMM result, at the result's own index, becomes one launch: the tile
+  // kernel evaluates the program on its accumulators (mfx_gemm_ew) and the
+  // GEMM result gets no buffer.  Run-time pointers the fused kernel does not
+  // take (alignment) fall back to the GEMM writing into the program's f32
+  // output, then the program in place there: same values, two launches.
+  void fuse_gemm_epilogues() {
+    std::vector<Step> steps;
+    std::vector<StepIO> io;
+    const size_t n = plan_.steps_.size();
+    for (size_t i = 0; i < n; ++i) {
+      if (i + 1 < n && try_fuse(i, steps, io)) {
+        ++i;
+        continue;
+      }
+      steps.push_back(std::move(plan_.steps_[i]));
+      io.push_back(io_[i]);
+    }
+    plan_.steps_ = std::move(steps);
+    io_ = std::move(io);
+  }
+
+  bool try_fuse(size_t i, std::vector<Step>& steps, std::vector<StepIO>& io) {
+    auto gi = gemm_meta_.find(i);
+    auto ei = ew_meta_.find(i + 1);
+    if (gi == gemm_meta_.end() || ei == ew_meta_.end()) return false;
+    const GemmMeta G = gi->second;
+    const EwMeta E = ei->second;
+    const int gv = resolve_alias(G.out_v);
+    if (E.prog.out_dtype != MFX_F32) return false;
+    for (int r : f_.results)
+      if (resolve_alias(r) == gv) return false;
+    for (size_t j = 0; j < io_.size(); ++j) {
+      if (j == i + 1) continue;
+      for (int v : io_[j].reads)
+        if (resolve_alias(v) == gv) return false;
+    }
+    int ci = -1;
+    for (size_t k = 0; k < E.ins.size(); ++k) {
+      if (resolve_alias(E.ins[k].value) != gv) continue;
+      if (ci >= 0 || E.ins[k].off != 0) return false;
+      ci = (int)k;
+    }
+    if (ci < 0) return false;
+    // Plan-time check with placeholder pointers of the run-time alignment
+    // (buffers are 256-byte aligned; views keep their byte offsets).
+    constexpr uintptr_t kBase = 1u << 20;
+    mfx_gemm_args g = G.g;
+    g.a = reinterpret_cast<const void*>(kBase + (uintptr_t)G.aoff);
+    g.b = reinterpret_cast<const void*>(kBase + (uintptr_t)G.boff);
+    g.c = nullptr;
+    mfx_ew_program p = E.prog;
+    p.out = reinterpret_cast<void*>(kBase);
+    for (size_t k = 0; k < E.ins.size(); ++k)
+      p.inputs[k].data =
+          reinterpret_cast<const void*>(kBase + (uintptr_t)(E.ins[k].off * elem_bytes(p.inputs[k].dtype)));
+    if (mfx_gemm_ew_check(&g, &p, ci) != MFX_OK) return false;
+    (void)mfx_gemm_ew_prepare(&g, &p, ci);  // compiles now when a device is current
+    Step s;
+    s.kind = "gemm_ew";
+    s.label = plan_.steps_[i].label + " + " + plan_.steps_[i + 1].label;
+    s.flops = plan_.steps_[i].flops;
+    s.bytes = plan_.steps_[i + 1].bytes;
+    auto loc = loc_;
+    Plan* plan = &plan_;
+    const mfx_gemm_args g0 = G.g;
+    const mfx_ew_program p0 = E.prog;
+    const std::vector<ProgIn> ins = E.ins;
+    const int out_value = E.out_value;
+    s.run = [G, g0, p0, ins, ci, out_value, loc, plan](const ExecBuffers& b, std::string& err) {
+      mfx_gemm_args a = g0;
+      a.a = (char*)plan->ptr((*loc)[G.av], b) + G.aoff;
+      a.b = (char*)plan->ptr((*loc)[G.bv], b) + G.boff;
+      a.c = nullptr;
+      mfx_ew_program p = p0;
+      p.out = plan->ptr((*loc)[out_value], b);
+      for (size_t k = 0; k < ins.size(); ++k) {
+        if ((int)k == ci) continue;
+        char* base = (char*)plan->ptr((*loc)[ins[k].value], b);
+        p.inputs[k].data = base + ins[k].off * elem_bytes(p.inputs[k].dtype);
+      }
+      int rc = mfx_gemm_ew(&a, &p, ci, b.stream);
+      if (rc == MFX_E_UNSUPPORTED) {
+        a.c = p.out;
+        rc = mfx_gemm(&a, b.stream);
+        if (rc == MFX_OK) {
+          p.inputs[ci].data = p.out;
+          rc = mfx_elementwise(&p, b.stream);
+        }
+      }
+      if (rc != MFX_OK) err = mfx_last_error();
+      return rc;
+    };
+    StepIO sio;
+    sio.reads = {G.av, G.bv};
+    for (size_t k = 0; k < ins.size(); ++k)
+      if ((int)k != ci) sio.reads.push_back(ins[k].value);
+    sio.writes = {out_value};
+    steps.push_back(std::move(s));
+    io.push_back(sio);
+    return true;
   }
 
   std::map<int, int> alias_of_;

@@ -131,6 +131,92 @@ class SdpaBwdArgs(ctypes.Structure):
     ]
 
 
+class GemmArgs(ctypes.Structure):
+    """mfx_gemm_args (include/mfx_kernels.h)."""
+
+    _fields_ = [
+        ("a", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("c", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("c_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("m", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("lda", ctypes.c_int64),
+        ("ldb", ctypes.c_int64),
+        ("ldc", ctypes.c_int64),
+        ("stride_a", ctypes.c_int64),
+        ("stride_b", ctypes.c_int64),
+        ("stride_c", ctypes.c_int64),
+        ("trans_a", ctypes.c_int32),
+        ("trans_b", ctypes.c_int32),
+    ]
+
+
+MFX_MAX_RANK = 8
+MFX_EW_MAX_INPUTS = 8
+MFX_EW_MAX_INSTRS = 64
+
+# Elementwise opcodes (enum order of include/mfx_kernels.h).
+EW_OPS = ["load", "const", "iota", "neg", "abs", "exp", "expm1", "log", "log1p", "sqrt", "rsqrt", "tanh",
+          "logistic", "erf", "sin", "cos", "floor", "ceil", "round_ne", "sign", "not", "round_bf16",
+          "round_f16", "to_int", "is_finite", "copy", "add", "sub", "mul", "div", "max", "min", "pow", "rem",
+          "and", "or", "xor", "eq", "ne", "lt", "le", "gt", "ge", "atan2", "select", "clamp"]
+EW_OP = {name: i for i, name in enumerate(EW_OPS)}
+
+
+class EwInstr(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_uint8), ("dst", ctypes.c_uint8), ("a", ctypes.c_uint8), ("b", ctypes.c_uint8),
+                ("c", ctypes.c_uint8), ("flags", ctypes.c_uint8), ("pad", ctypes.c_uint8 * 2),
+                ("imm", ctypes.c_float)]
+
+
+class EwInput(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("strides", ctypes.c_int64 * MFX_MAX_RANK)]
+
+
+class EwProgram(ctypes.Structure):
+    """mfx_ew_program (include/mfx_kernels.h)."""
+
+    _fields_ = [("out", ctypes.c_void_p), ("out_dtype", ctypes.c_int32), ("rank", ctypes.c_int32),
+                ("dims", ctypes.c_int64 * MFX_MAX_RANK), ("out_strides", ctypes.c_int64 * MFX_MAX_RANK),
+                ("num_inputs", ctypes.c_int32), ("num_instrs", ctypes.c_int32), ("result", ctypes.c_int32),
+                ("pad", ctypes.c_int32), ("inputs", EwInput * MFX_EW_MAX_INPUTS),
+                ("code", EwInstr * MFX_EW_MAX_INSTRS)]
+
+
+def ew_program(dims, inputs, code, result, out_dtype=MFX_F32):
+    """Builds an EwProgram.  inputs: [(dtype_code, strides)] (data pointers
+    are set by the caller); code: [(op_name, dst, a, b, c, imm)] with
+    trailing fields optional (0, and imm 0.0); result: register of the
+    output."""
+    p = EwProgram()
+    p.out_dtype = out_dtype
+    p.rank = len(dims)
+    for d, x in enumerate(dims):
+        p.dims[d] = x
+    p.num_inputs = len(inputs)
+    for i, (dt, strides) in enumerate(inputs):
+        p.inputs[i].dtype = dt
+        for d, x in enumerate(strides):
+            p.inputs[i].strides[d] = x
+    p.num_instrs = len(code)
+    for pc, ins in enumerate(code):
+        op, dst, *rest = ins
+        a, b, c, imm = list(rest) + [0, 0, 0, 0.0][len(rest):]
+        p.code[pc].op = EW_OP[op]
+        p.code[pc].dst = dst
+        p.code[pc].a = a
+        p.code[pc].b = b
+        p.code[pc].c = c
+        p.code[pc].imm = imm
+    p.result = result
+    return p
+
+
 _lib = None
 
 
@@ -169,6 +255,21 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.mfx_sdpa_workspace_size.restype = ctypes.c_size_t
     lib.mfx_sdpa_kernel_name.argtypes = [ctypes.POINTER(SdpaArgs)]
     lib.mfx_sdpa_kernel_name.restype = ctypes.c_char_p
+    lib.mfx_gemm.argtypes = [ctypes.POINTER(GemmArgs), ctypes.c_void_p]
+    lib.mfx_gemm.restype = ctypes.c_int
+    lib.mfx_gemm_kernel_name.argtypes = [ctypes.POINTER(GemmArgs)]
+    lib.mfx_gemm_kernel_name.restype = ctypes.c_char_p
+    lib.mfx_gemm_ew.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(EwProgram), ctypes.c_int, ctypes.c_void_p]
+    lib.mfx_gemm_ew.restype = ctypes.c_int
+    lib.mfx_gemm_ew_check.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(EwProgram), ctypes.c_int]
+    lib.mfx_gemm_ew_check.restype = ctypes.c_int
+    lib.mfx_gemm_ew_prepare.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(EwProgram), ctypes.c_int]
+    lib.mfx_gemm_ew_prepare.restype = ctypes.c_int
+    lib.mfx_gemm_ew_source.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(EwProgram), ctypes.c_int,
+                                       ctypes.c_char_p, ctypes.c_int64]
+    lib.mfx_gemm_ew_source.restype = ctypes.c_int64
+    lib.mfx_elementwise.argtypes = [ctypes.POINTER(EwProgram), ctypes.c_void_p]
+    lib.mfx_elementwise.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -465,3 +566,91 @@ def sdpa_bwd_kernel_name(q, k, v, **kw) -> str:
 def sdpa_bwd_workspace_size(q, k, v, **kw) -> int:
     a = sdpa_bwd_args(q, k, v, q, q, k, v, **kw)
     return int(load().mfx_sdpa_bwd_workspace_size(ctypes.byref(a)))
+
+
+# ---- GEMM ----------------------------------------------------------------------
+
+def _matrix(x):
+    """(batch, rows, cols, ld, batch_stride) of a 2-D or 3-D tensor whose
+    last dim is contiguous."""
+    if x.dim() not in (2, 3) or x.stride(-1) != 1:
+        raise ValueError("GEMM operands are 2-D or 3-D with a contiguous last dim")
+    if x.dim() == 2:
+        return 1, x.shape[0], x.shape[1], x.stride(0), 0
+    return x.shape[0], x.shape[1], x.shape[2], x.stride(1), x.stride(0)
+
+
+def gemm_args(a, b, c=None):
+    """GemmArgs for c = a @ b (row-major, optionally batched; b may be 2-D
+    and shared by every batch of a)."""
+    ba, m, k, lda, sa = _matrix(a)
+    bb, k2, n, ldb, sb = _matrix(b)
+    if k2 != k or (bb != ba and bb != 1):
+        raise ValueError("GEMM extents disagree")
+    g = GemmArgs()
+    g.a, g.b = a.data_ptr(), b.data_ptr()
+    g.c = c.data_ptr() if c is not None else None
+    g.dtype = dtype_code(a.dtype)
+    g.c_dtype = dtype_code(c.dtype) if c is not None else MFX_F32
+    g.batch, g.m, g.n, g.k = ba, m, n, k
+    g.lda, g.ldb, g.ldc = lda, ldb, n
+    g.stride_a, g.stride_b, g.stride_c = sa, (sb if bb > 1 else 0), m * n
+    return g
+
+
+def gemm(a, b, out=None):
+    """mfx_gemm: a [(batch,) m, k] @ b [(batch,) k, n] into a new contiguous
+    f32 tensor (or `out`)."""
+    torch = _torch()
+    _require_gpu(a, b)
+    batch = a.shape[0] if a.dim() == 3 else None
+    shape = (batch, a.shape[-2], b.shape[-1]) if batch is not None else (a.shape[-2], b.shape[-1])
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=a.device)
+    g = gemm_args(a, b, out)
+    check(load().mfx_gemm(ctypes.byref(g), _stream_handle(a)))
+    return out
+
+
+def gemm_kernel_name(a, b, out=None) -> str:
+    """Kernel mfx_gemm runs for a @ b: "gemm_f32_tile" or "rocblas"."""
+    return load().mfx_gemm_kernel_name(ctypes.byref(gemm_args(a, b, out))).decode()
+
+
+def _bind_inputs(prog, tensors):
+    keep = []
+    for i, t in enumerate(tensors):
+        prog.inputs[i].data = t.data_ptr() if t is not None else None
+        keep.append(t)
+    return keep
+
+
+def gemm_ew(a, b, prog, c_input, inputs, out):
+    """mfx_gemm_ew: out = prog(inputs) with inputs[c_input] the product a @ b
+    (pass None for it)."""
+    _require_gpu(a, b, out)
+    g = gemm_args(a, b)
+    prog.out = out.data_ptr()
+    _bind_inputs(prog, inputs)
+    check(load().mfx_gemm_ew(ctypes.byref(g), ctypes.byref(prog), c_input, _stream_handle(a)))
+    return out
+
+
+def elementwise(prog, inputs, out):
+    """mfx_elementwise: out = prog(inputs)."""
+    _require_gpu(out)
+    prog.out = out.data_ptr()
+    _bind_inputs(prog, inputs)
+    check(load().mfx_elementwise(ctypes.byref(prog), _stream_handle(out)))
+    return out
+
+
+def gemm_ew_source(g, prog, c_input) -> str | None:
+    """Generated source of the fused kernel (None when the pair is not fused)."""
+    lib = load()
+    n = lib.mfx_gemm_ew_source(ctypes.byref(g), ctypes.byref(prog), c_input, None, 0)
+    if n < 0:
+        return None
+    buf = ctypes.create_string_buffer(int(n) + 1)
+    lib.mfx_gemm_ew_source(ctypes.byref(g), ctypes.byref(prog), c_input, buf, n + 1)
+    return buf.value.decode()

@@ -592,6 +592,35 @@ def transformer_module(layers=4, B=32, T=256, d=512, heads=8, mlp=2048, eps=1e-5
     return module("jit_transformer", [f.text([x], [ty(xs, dt)])] + funcs)
 
 
+def dense_module(M=256, K=128, N=192, epilogue="bias", dt="f32", escape=None):
+    """One dense layer y = x @ w followed by its epilogue: "bias" (y + b),
+    "bias_gelu" (tanh GELU of y + b), "bias_residual" (r + (y + b)).
+    escape="result" also returns y; escape="reader" also returns y * 2 (a
+    second program reading y).  Arguments: x [M, K], w [K, N], b [N] and, for
+    bias_residual, r [M, N]."""
+    args = [([M, K], dt), ([K, N], dt), ([N], dt)]
+    if epilogue == "bias_residual":
+        args.append(([M, N], dt))
+    f = Fn("main", args)
+    y, ys = f.dot_general(f.arg(0), f.arg(1), [M, K], [K, N], ([], []), ([1], [0]), dt)
+    u = f.binary("add", y, f.bcast(f.arg(2), [N], [1], ys, dt), ys, dt)
+    if epilogue == "bias_gelu":
+        x3 = f.binary("multiply", f.binary("multiply", u, u, ys, dt), u, ys, dt)
+        inner = f.binary("add", u, f.binary("multiply", f.splat(0.044715, ys, dt), x3, ys, dt), ys, dt)
+        inner = f.binary("multiply", f.splat(math.sqrt(2.0 / math.pi), ys, dt), inner, ys, dt)
+        t = f.unary("tanh", inner, ys, dt)
+        u = f.binary("multiply", f.binary("multiply", f.splat(0.5, ys, dt), u, ys, dt),
+                     f.binary("add", f.splat(1.0, ys, dt), t, ys, dt), ys, dt)
+    elif epilogue == "bias_residual":
+        u = f.binary("add", f.arg(3), u, ys, dt)
+    outs = [u]
+    if escape == "result":
+        outs.append(y)
+    elif escape == "reader":
+        outs.append(f.binary("multiply", y, f.splat(2.0, ys, dt), ys, dt))
+    return module("jit_dense", [f.text(outs, [ty(ys, dt)] * len(outs))])
+
+
 def config4_inputs(seed=4, layers=4, B=32, T=256, d=512, mlp=2048):
     """Arguments of transformer_module in order, as BASELINE config 4 states
     them: x ~ N(0,1), Xavier-uniform weights (U(+-sqrt(6 / (fan_in +

@@ -146,3 +146,93 @@ def test_calls_fail_loudly_without_a_gpu(native):
     x = torch.zeros(4, 8)
     with pytest.raises(ValueError):
         native.layer_norm(x)
+
+
+# ---------------------------------------------------------------- GEMM
+
+def test_gemm_kernel_selection(native):
+    """f32 row-major products go to the hand-written MFMA tile kernel; what it
+    does not take (bf16, K % 4, odd N, rows not 16-byte aligned) to rocBLAS."""
+    import torch
+
+    f = torch.float32
+    a, b = torch.zeros(8192, 512, dtype=f), torch.zeros(512, 1536, dtype=f)
+    assert native.gemm_kernel_name(a, b) == "gemm_f32_tile"
+    assert native.gemm_kernel_name(torch.zeros(3, 100, 64, dtype=f), torch.zeros(3, 64, 96, dtype=f)) == "gemm_f32_tile"
+    assert native.gemm_kernel_name(a.bfloat16(), b.bfloat16()) == "rocblas"
+    assert native.gemm_kernel_name(torch.zeros(64, 6, dtype=f), torch.zeros(6, 64, dtype=f)) == "rocblas"
+    assert native.gemm_kernel_name(torch.zeros(64, 8, dtype=f), torch.zeros(8, 63, dtype=f)) == "rocblas"
+    flat = torch.zeros(64 * 8 + 1, dtype=f)
+    assert native.gemm_kernel_name(flat[1:].view(64, 8), torch.zeros(8, 64, dtype=f)) == "rocblas"
+
+
+def _fused_pair(native, name, dims, K):
+    import gemm_programs as gp
+
+    prog, ci, extras = gp.PROGRAMS[name](dims)
+    rows = 1
+    for d in dims[:-1]:
+        rows *= d
+    g = native.GemmArgs()
+    g.a, g.b = 1 << 20, 1 << 21
+    g.dtype = g.c_dtype = native.MFX_F32
+    g.batch, g.m, g.n, g.k = 1, rows, dims[-1], K
+    g.lda, g.ldb, g.ldc, g.stride_c = K, dims[-1], dims[-1], rows * dims[-1]
+    prog.out = 1 << 22
+    for i in range(prog.num_inputs):
+        prog.inputs[i].data = (1 << 23) + 4096 * i
+    return g, prog, ci
+
+
+@pytest.mark.parametrize("name,dims,K", [("bias_gelu", [8192, 2048], 512), ("mixed", [3, 5, 64], 36)])
+def test_gemm_epilogue_source_compiles(native, tmp_path, name, dims, K):
+    """The generated fused kernel (program as epilogue of the tile kernel)
+    compiles for gfx950 with the options hipRTC gets, without spilling."""
+    import subprocess
+
+    g, prog, ci = _fused_pair(native, name, dims, K)
+    lib = native.load()
+    assert lib.mfx_gemm_ew_check(ctypes.byref(g), ctypes.byref(prog), ci) == 0
+    src = native.gemm_ew_source(g, prog, ci)
+    assert src and "mfx_gemm_ew_kernel" in src
+    (tmp_path / "k.hip").write_text(src)
+    out = tmp_path / "k.s"
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                        "-I", str(REPO / "jax-mlx-plugin_amd/csrc/kernels"), str(tmp_path / "k.hip"), "-o", str(out)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    asm = out.read_text()
+    assert re.search(r"\.vgpr_spill_count:\s+0", asm) and "v_mfma_f32_32x32x2_f32" in asm
+
+
+def test_gemm_epilogue_rejections(native):
+    """mfx_gemm_ew_check refuses what the fused kernel cannot do."""
+    import gemm_programs as gp
+
+    lib = native.load()
+
+    def rc(g, prog, ci):
+        return lib.mfx_gemm_ew_check(ctypes.byref(g), ctypes.byref(prog), ci)
+
+    g, prog, ci = _fused_pair(native, "bias_residual", [256, 192], 128)
+    assert rc(g, prog, ci) == 0
+    assert rc(g, prog, 7) == -1                       # c_input out of range
+    prog.inputs[ci].strides[0], prog.inputs[ci].strides[1] = 1, 256
+    assert rc(g, prog, ci) == -2                      # product read transposed
+    g, prog, ci = _fused_pair(native, "bias_residual", [256, 192], 128)
+    prog.out_strides[0], prog.out_strides[1] = 1, 256
+    assert rc(g, prog, ci) == -2                      # strided output
+    g, prog, ci = _fused_pair(native, "bias_residual", [256, 192], 128)
+    prog.out = (1 << 22) + 4
+    assert rc(g, prog, ci) == -2                      # output not aligned to an element pair
+    g, prog, ci = _fused_pair(native, "bias_residual", [256, 192], 128)
+    g.a = (1 << 20) + 4
+    assert rc(g, prog, ci) == -2                      # A rows not 16-byte aligned
+    # index space [512, 96]: no dim boundary at N = 192
+    prog, ci, _ = gp.bias_add([512, 96])
+    g, _, _ = _fused_pair(native, "bias_add", [256, 192], 128)
+    prog.out = 1 << 22
+    for i in range(prog.num_inputs):
+        prog.inputs[i].data = (1 << 23) + 4096 * i
+    assert rc(g, prog, ci) == -2

@@ -404,9 +404,35 @@ def test_transformer_plan(api):
     ops = [n["op"] for n in fused(d)]
     assert ops.count("mfx.layer_norm") == 4 and ops.count("mfx.sdpa") == 2
     s = steps(d)
-    assert s.count("gemm") == 8 and s.count("sdpa") == 2 and s.count("layer_norm") == 4
+    # every dot_general carries its bias / residual / GELU program as a fused epilogue
+    assert s.count("gemm_ew") == 8 and s.count("sdpa") == 2 and s.count("layer_norm") == 4
+    assert "gemm" not in s and "elementwise" not in s
     sd = [n for n in fused(d) if n["op"] == "mfx.sdpa"][0]
     assert sd["i:offsets"] == [0, 128, 256, 0]  # q, k, v read in place from the QKV projection
+
+
+@pytest.mark.parametrize("epilogue", ["bias", "bias_gelu", "bias_residual"])
+def test_dense_epilogue_fuses_into_gemm(api, epilogue):
+    """A dot_general whose only reader is one elementwise program at the
+    product's own index runs as one fused GEMM launch."""
+    d = api.inspect(M.dense_module(epilogue=epilogue))
+    assert steps(d) == ["gemm_ew"]
+
+
+@pytest.mark.parametrize("escape", ["result", "reader"])
+def test_dense_epilogue_not_fused_when_product_escapes(api, escape):
+    """The product stays materialised when it is also a result, or when a
+    second program reads it."""
+    s = steps(api.inspect(M.dense_module(epilogue="bias_gelu", escape=escape)))
+    assert s[0] == "gemm" and "gemm_ew" not in s and s.count("elementwise") >= 1
+
+
+def test_dense_epilogue_rules(api):
+    """Products the f32 tile kernel does not take keep two steps: bf16
+    operands, K not a multiple of 4, odd N."""
+    for kw in (dict(dt="bf16"), dict(K=126), dict(N=191)):
+        s = steps(api.inspect(M.dense_module(**kw)))
+        assert s == ["gemm", "elementwise"], (kw, s)
 
 
 def test_parse_errors(api):

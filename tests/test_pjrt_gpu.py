@@ -438,6 +438,62 @@ def test_transformer_config4_full_size(client, oracle):
     assert err <= F32_SDPA_TOL, err
 
 
+def dense_ref(x, w, b, epilogue, r=None):
+    u = x.astype(np.float64) @ w.astype(np.float64) + b
+    if epilogue == "bias_gelu":
+        return 0.5 * u * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (u + 0.044715 * u ** 3)))
+    if epilogue == "bias_residual":
+        return r + u
+    return u
+
+
+def dense_args(rng, m, k, n, epilogue):
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((k, n)) / math.sqrt(k)).astype(np.float32)
+    b = (0.5 * rng.standard_normal(n)).astype(np.float32)
+    return [x, w, b] + ([rng.standard_normal((m, n)).astype(np.float32)] if epilogue == "bias_residual" else [])
+
+
+@pytest.mark.parametrize("epilogue", ["bias", "bias_gelu", "bias_residual"])
+def test_dense_epilogue_fused(client, epilogue):
+    """dot_general + its bias / GELU / residual program, planned as one fused
+    launch (gemm_ew), against the fp64 dense layer.  Bar 2e-5 max-abs on
+    O(1) outputs (fp32 accumulation over K = 256 plus the epilogue's own
+    rounding)."""
+    rng = np.random.default_rng(31)
+    args = dense_args(rng, 512, 256, 384, epilogue)
+    (y,) = run(client, M.dense_module(M=512, K=256, N=384, epilogue=epilogue), args, ["f32"] * len(args))
+    ref = dense_ref(*args[:3], epilogue, *(args[3:] or [None]))
+    assert np.abs(y - ref).max() <= 2e-5
+
+
+def test_dense_epilogue_unaligned_weights_fall_back(client):
+    """Weights passed as a device view 4 bytes off 16-byte alignment: the
+    fused kernel does not take them, so the step runs the GEMM into its
+    output and the program in place there -- the same values within the
+    f32 bar, and a result equal to the aligned run's to 1e-5."""
+    import torch
+
+    rng = np.random.default_rng(32)
+    args = dense_args(rng, 256, 128, 192, "bias_gelu")
+    exe = client.compile(M.dense_module(M=256, K=128, N=192, epilogue="bias_gelu"))
+    x, w, b = (torch.from_numpy(a).cuda() for a in args)
+    flat = torch.zeros(w.numel() + 1, device="cuda")
+    flat[1:] = w.flatten()
+    w_off = flat[1:].view(w.shape)
+    assert w_off.data_ptr() % 16 == 4
+    outs = []
+    for wv in (w, w_off):
+        (o,) = exe.execute([client.buffer_view(x), client.buffer_view(wv), client.buffer_view(b)])
+        outs.append(o.to_torch().double().numpy())
+        o.destroy()
+    exe.destroy()
+    ref = dense_ref(*args, "bias_gelu")
+    for y in outs:
+        assert np.abs(y - ref).max() <= 2e-5
+    assert np.abs(outs[0] - outs[1]).max() <= 1e-5
+
+
 def test_escaping_intermediates_layer_norm(client, oracle):
     """Escape guard (reference src/jax_mlx_pjrt.cpp:1843-1855): a LayerNorm
     whose mean and variance are also results.  The fusion fires and the
