@@ -340,6 +340,45 @@ def bench_config4(torch, steps, warmup):
     return res
 
 
+def bench_config4_gemms(torch, native, steps, warmup):
+    """Config 4's four dense layers one at a time, as the plan runs them: the
+    f32 tile GEMM with its elementwise consumer fused (mfx_gemm_ew: QKV +
+    bias; out-proj + bias + residual; MLP-in + bias + tanh GELU; MLP-out +
+    bias + residual), beside the plain tile GEMM (mfx_gemm) and torch.matmul
+    (hipBLASLt) of the same product.  Inputs from default_rng(4).  Device
+    time per call from graph replay (the eager figure adds Python's per-call
+    marshalling); TFLOP/s counts the product only."""
+    import numpy as np
+
+    import gemm_programs as gp
+
+    rng = np.random.default_rng(4)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()  # noqa: E731
+    out = {}
+    for label, name, n, k in (("qkv", "bias_add", 1536, 512), ("out_proj", "bias_residual", 512, 512),
+                              ("mlp_in", "bias_gelu", 2048, 512), ("mlp_out", "bias_residual", 512, 2048)):
+        m = 8192
+        a, b = dev(rng.standard_normal((m, k))), dev(rng.standard_normal((k, n)) / np.sqrt(k))
+        prog, ci, extras = gp.PROGRAMS[name]([m, n])
+        ext = [dev(rng.standard_normal(shape)) for _, shape, _, _ in extras]
+        inputs, it = [], iter(ext)
+        for i in range(prog.num_inputs):
+            inputs.append(None if i == ci else next(it))
+        y, c = torch.empty(m, n, device="cuda"), torch.empty(m, n, device="cuda")
+        fns = {"fused": lambda: native.gemm_ew(a, b, prog, ci, inputs, y),
+               "tile_gemm": lambda: native.gemm(a, b, c),
+               "torch_matmul": lambda: torch.matmul(a, b)}
+        flops = 2.0 * m * n * k
+        res = {"shape": [m, n, k], "epilogue": name}
+        for key, fn in fns.items():
+            avg_ms, _, _ = time_launches(torch, fn, steps, warmup)
+            g_us = graph_replay_us(torch, fn, reps=20)
+            res[key] = {"eager_us": round(avg_ms * 1e3, 2), "device_us": round(g_us, 2) if g_us else None,
+                        "TFLOPs": round(flops / ((g_us or avg_ms * 1e3) * 1e-6) / 1e12, 1)}
+        out[label] = res
+    return out
+
+
 def bench_config3_bwd(torch, native, steps, warmup):
     """mfx_sdpa_bwd on the config-3 shape (causal bf16 [4,32,2048,128]): the
     recomputed forward (O and lse), delta, dK/dV and dQ.  TFLOP/s uses the
@@ -395,6 +434,7 @@ ONLY = {
     "config2": lambda torch, native, k, w: bench_config2(torch, native, k, w),
     "config3": lambda torch, native, k, w: bench_config3(torch, native, k, w),
     "config4": lambda torch, native, k, w: bench_config4(torch, k, w),
+    "config4_gemm": lambda torch, native, k, w: bench_config4_gemms(torch, native, k, w),
     "config5": lambda torch, native, k, w: bench_config5(torch, native, k, w),
     "ln_sweep": lambda torch, native, k, w: {
         "sweep": [bench_layer_norm(torch, native, 1 << 20, 512, k, w),
@@ -508,6 +548,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("config 4: 4-layer transformer forward through PJRT")
         extra["config4_transformer_pjrt"] = bench_config4(torch, 20, 3)
+        torch.cuda.empty_cache()
+        log("config 4 dense layers: fused tile GEMM vs plain tile GEMM vs torch.matmul")
+        extra["config4_gemms"] = bench_config4_gemms(torch, native, 20, 3)
         torch.cuda.empty_cache()
         line["extra"] = extra
 
