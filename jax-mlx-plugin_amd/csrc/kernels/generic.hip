@@ -8,6 +8,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "ew_math.h"
 
 namespace mfx {
 namespace {
@@ -101,7 +102,7 @@ __device__ __forceinline__ void apply_n(const mfx_ew_instr& in, Opnd&& opnd, flo
     case MFX_EW_LOG1P: MFX_EW_UN_SLOW(log1pf(a))
     case MFX_EW_SQRT: MFX_EW_UN(sqrtf(a))
     case MFX_EW_RSQRT: MFX_EW_UN(1.0f / sqrtf(a))
-    case MFX_EW_TANH: MFX_EW_UN_SLOW(tanhf(a))
+    case MFX_EW_TANH: MFX_EW_UN(mfx_tanh(a))
     case MFX_EW_LOGISTIC: MFX_EW_UN_SLOW(1.0f / (1.0f + expf(-a)))
     case MFX_EW_ERF: MFX_EW_UN_SLOW(erff(a))
     case MFX_EW_SIN: MFX_EW_UN_SLOW(sinf(a))

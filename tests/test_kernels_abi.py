@@ -236,3 +236,37 @@ def test_gemm_epilogue_rejections(native):
     for i in range(prog.num_inputs):
         prog.inputs[i].data = (1 << 23) + 4096 * i
     assert rc(g, prog, ci) == -2
+
+
+def test_tanh_formula_accuracy():
+    """ew_math.h's mfx_tanh restated in numpy fp32 (the header's own
+    coefficients, fma as one rounding, exp2 and reciprocal correctly
+    rounded): within 2.5 ulp of fp64 tanh on a dense grid of [0, 20] and at
+    the 0.55 switch (the six roundings of the exp2 branch reach 2.2 ulp near
+    |x| = 1; the polynomial 0.8).  A wrong coefficient or a dropped term fails it by
+    orders of magnitude; the GPU test bounds the hardware's exp2 / rcp."""
+    import numpy as np
+
+    text = (REPO / "jax-mlx-plugin_amd/csrc/kernels/ew_math.h").read_text()
+    nums = [float(v) for v in re.findall(r"(-?\d+\.\d+)f", text)]
+    c4, c3, c2, c1, c0 = nums[0], nums[1], nums[2], nums[3], nums[4]
+    k, cut = nums[5], nums[-1]
+    assert cut == 0.55 and abs(k + 2.0 / np.log(2.0)) < 1e-12
+    f32 = np.float32
+
+    def fma(a, b, c):
+        return (a.astype(np.float64) * b + c).astype(f32)
+
+    x = np.concatenate([np.linspace(0, 20, 4_000_001, dtype=np.float64).astype(f32),
+                        np.nextafter(f32(0.55), f32(0)) + np.arange(-50, 50, dtype=f32) * np.spacing(f32(0.55))])
+    s = (x * x).astype(f32)
+    p = fma(np.full_like(s, c4), s, f32(c3))
+    for c in (c2, c1, c0):
+        p = fma(p, s, f32(c))
+    small = fma((x * s).astype(f32), p, x)
+    e = np.exp2((x * f32(k)).astype(f32).astype(np.float64)).astype(f32)
+    big = ((f32(1) - e) * (1.0 / (f32(1) + e).astype(np.float64)).astype(f32)).astype(f32)
+    y = np.where(x < f32(cut), small, big)
+    ref = np.tanh(x.astype(np.float64))
+    ulp = np.abs(y - ref) / np.spacing(np.maximum(np.abs(ref), 1e-38).astype(f32)).astype(np.float64)
+    assert ulp.max() <= 2.5, ulp.max()

@@ -652,3 +652,48 @@ def test_sdpa_bwd_config3_full_size(cuda, nat, oracle):
         for name, o, r in zip(("dq", "dk", "dv"), (dq, dk, dv), refs):
             rr = rel_inf(sl(o), r)
             assert rr <= BF16_REL_TOL, (b, h, name, rr)
+
+
+# ---------------------------------------------------------------- elementwise device math
+
+def test_tanh_device_accuracy_and_paths(cuda):
+    """stablehlo.tanh as the elementwise kernels compute it (ew_math.h's
+    mfx_tanh): the generated kernel and the interpreter give the same bits,
+    and every result is within 4 ulp of fp64 tanh on 2^22 points spread over
+    the f32 magnitudes (subnormals to 1e4), both signs, the 0.55 switch and
+    the specials (+-0, +-inf -> +-1, NaN -> NaN)."""
+    import numpy as np
+
+    from jax_mlx_amd import native as nt
+
+    torch = cuda
+    rng = np.random.default_rng(7)
+    mags = np.exp(rng.uniform(np.log(1e-40), np.log(1e4), 1 << 22)).astype(np.float32)
+    x = mags * np.where(rng.random(mags.size) < 0.5, -1, 1).astype(np.float32)
+    edge = np.float32(0.55) + np.arange(-64, 64, dtype=np.float32) * np.spacing(np.float32(0.55))
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 44.0, -44.0, 1e-45], dtype=np.float32)
+    x = np.concatenate([x, edge, -edge, special]).astype(np.float32)
+    n = x.size - x.size % 4
+    x = x[:n]
+    xd = torch.from_numpy(x).cuda()
+    prog = nt.ew_program([n], [(nt.MFX_F32, [1])], [("load", 0, 0), ("tanh", 1, 0)], 1)
+    outs = []
+    lib = nt.load()
+    for jit in (1, 0):
+        prev = lib.mfx_ew_jit_enable(jit)
+        try:
+            y = torch.empty_like(xd)
+            nt.elementwise(prog, [xd], y)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+        finally:
+            lib.mfx_ew_jit_enable(prev)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    y = outs[0]
+    ref = np.tanh(x.astype(np.float64))
+    fin = np.isfinite(x)
+    ulp = np.abs(y[fin] - ref[fin]) / np.spacing(np.maximum(np.abs(ref[fin]), 1e-38).astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 4.0, (ulp.max(), x[fin][np.argmax(ulp)])
+    assert np.isnan(y[np.isnan(x)]).all()
+    assert (y[x == np.inf] == 1).all() and (y[x == -np.inf] == -1).all()
+    assert np.signbit(y[(x == 0) & np.signbit(x)]).all()
