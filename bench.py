@@ -380,24 +380,39 @@ def bench_config4_gemms(torch, native, steps, warmup):
 
 
 def bench_config3_bwd(torch, native, steps, warmup):
-    """mfx_sdpa_bwd on the config-3 shape (causal bf16 [4,32,2048,128]): the
-    recomputed forward (O and lse), delta, dK/dV and dQ.  TFLOP/s uses the
-    FlashAttention-2 convention of 2.5x the forward's causal FLOPs (the five
-    backward products S, dP, dV, dQ, dK), so the recompute is overhead."""
+    """mfx_sdpa_bwd on the config-3 shape (causal bf16 [4,32,2048,128]) two
+    ways.  As the custom_call @mlx_sdpa_bwd interface runs it (q, k, v and
+    the output gradient only): the recomputed forward (O and lse), delta,
+    dK/dV and dQ.  From a forward's residuals (`from_forward`): the forward
+    call's output and lse passed in, as the plan does for a forward and its
+    backward in one module (the forward runs once, outside the timed calls).
+    TFLOP/s uses the FlashAttention-2 convention of 2.5x the forward's causal
+    FLOPs (the five backward products S, dP, dV, dQ, dK), so a recompute is
+    overhead."""
     import numpy as np
 
     B, H, T, d = 4, 32, 2048, 128
     rng = np.random.default_rng(3)
     q, k, v, g = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32))
                   .to("cuda").bfloat16() for _ in range(4))
-    ws = torch.empty(native.sdpa_bwd_workspace_size(q, k, v, causal=True), dtype=torch.uint8, device="cuda")
-    fn = lambda: native.sdpa_bwd(q, k, v, g, causal=True, workspace=ws)  # noqa: E731
-    avg_ms, med_ms, _ = time_launches(torch, fn, steps, warmup)
     flops = 2.5 * sdpa_causal_flops(B, H, T, d)
-    return {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "flops_fa2_convention": flops,
-            "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
-            "frac_bf16_peak": flops / (avg_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-            "kernel": native.sdpa_bwd_kernel_name(q, k, v, causal=True)}
+
+    def figures(fn):
+        avg_ms, med_ms, _ = time_launches(torch, fn, steps, warmup)
+        return {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3, "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
+                "frac_bf16_peak": flops / (avg_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+
+    ws = torch.empty(native.sdpa_bwd_workspace_size(q, k, v, causal=True), dtype=torch.uint8, device="cuda")
+    res = figures(lambda: native.sdpa_bwd(q, k, v, g, causal=True, workspace=ws))
+    res["flops_fa2_convention"] = flops
+    res["kernel"] = native.sdpa_bwd_kernel_name(q, k, v, causal=True)
+    lse = torch.empty(B * H * T, dtype=torch.float32, device="cuda")
+    out = native.sdpa(q, k, v, causal=True, lse=lse)
+    ws2 = torch.empty(native.sdpa_bwd_workspace_size(q, k, v, causal=True, fwd_out=out, fwd_lse=lse),
+                      dtype=torch.uint8, device="cuda")
+    res["from_forward"] = figures(lambda: native.sdpa_bwd(q, k, v, g, causal=True, workspace=ws2, fwd_out=out,
+                                                          fwd_lse=lse))
+    return res
 
 
 def bench_layer_norm_bwd(torch, native, rows, n, steps, warmup, seed=1):

@@ -164,6 +164,12 @@ size_t mfx_layer_norm_bwd_workspace_size(const mfx_norm_bwd_args* args);
  * probabilities feed the PV product in the bf16 path, as JAX's attention
  * casts them to the value dtype).
  *
+ * lse (optional output): the row log-sum-exp of the scaled, masked scores in
+ * log2 units, lse[(b * Hq + h) * Tq + i] = log2(sum_j exp2(log2e * (scale *
+ * q_i.k_j + M_ij))), fp32 -- what mfx_sdpa_bwd needs (fwd_lse) to skip its
+ * recomputed forward pass.  When it is set the split-KV decode kernels (which
+ * do not form it) are not used.  NULL: not written.
+ *
  * workspace: split-KV decode keeps per-split partial results there.  Query
  * the size with mfx_sdpa_workspace_size(); pass NULL to let the library use a
  * per-device buffer it allocates once and reuses (calls that overlap on one
@@ -193,6 +199,7 @@ typedef struct {
   int32_t dtype;
   int32_t mask_dtype;
   int32_t reserved;
+  float* lse;
 } mfx_sdpa_args;
 
 int mfx_sdpa_fwd(const mfx_sdpa_args* args, void* stream);
@@ -233,8 +240,18 @@ const char* mfx_sdpa_kernel_name(const mfx_sdpa_args* args);
  * dq / dk / dv have q / k / v's logical shapes and their own strides, and
  * every tensor has `dtype` (fp32 accumulation).  The forward pass is
  * recomputed into the workspace (out and the row log-sum-exp), so only the
- * inputs are needed.  Workspace: mfx_sdpa_bwd_workspace_size() bytes, or
- * NULL for library scratch.  Deterministic: no atomics.
+ * inputs are needed -- unless the caller passes the forward's own results:
+ * fwd_out (out of mfx_sdpa_fwd on the same inputs, `dtype`, strides
+ * fwd_out_strides) and fwd_lse (that call's lse output), both or neither;
+ * with both, the recompute is skipped.  The gradients then equal the
+ * recomputing call's bit for bit whenever the forward ran the kernel the
+ * recompute runs (out 16-byte aligned with strides a multiple of 4 -- every
+ * output the plugin's planner allocates).  A plan that
+ * runs a forward and its backward passes them along; the reference's
+ * custom_call @mlx_sdpa_bwd interface (q, k, v, grad_out) has no slot for
+ * them, and its mx::vjp recomputes.  Workspace:
+ * mfx_sdpa_bwd_workspace_size() bytes, or NULL for library scratch.
+ * Deterministic: no atomics.
  * Replaces mx::vjp of fast::scaled_dot_product_attention behind custom_call
  * @mlx_sdpa_bwd (reference src/jax_mlx_pjrt.cpp:8151-8206; closed form
  * src/jax_mlx/sdpa.py:65-87).
@@ -263,6 +280,9 @@ typedef struct {
   int32_t causal;
   int32_t dtype;
   int32_t mask_dtype;
+  const void* fwd_out;
+  const float* fwd_lse;
+  int64_t fwd_out_strides[4];
 } mfx_sdpa_bwd_args;
 
 int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream);

@@ -73,8 +73,13 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
   p.q_rms_eps = a->q_rms_eps;
   p.num_splits = 1;
   p.split_len = p.Tk;
+  // The row log-sum-exp output, for a backward pass: the split-KV decode
+  // kernels do not form it, so a request for it takes the flash / generic
+  // kernels.
+  p.lse = a->lse;
+  const bool decode_ok = a->lse == nullptr;
 
-  if (p.Tq <= 4 && decode_mfma_supports(p)) {
+  if (decode_ok && p.Tq <= 4 && decode_mfma_supports(p)) {
     // W wavefronts split the listed (visible) tiles of all kv heads into
     // equal ranges: as many as stay resident at once, at most one per tile.
     out.kind = Kind::kDecodeMfma;
@@ -84,7 +89,7 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
     out.partial_bytes = decode_mfma_workspace(p, out.decode_waves);
     return MFX_OK;
   }
-  if (p.Tq <= 4 && decode_supports(p)) {
+  if (decode_ok && p.Tq <= 4 && decode_supports(p)) {
     out.kind = Kind::kDecode;
     const int pairs = p.B * p.Hkv;
     int splits = (2048 + pairs - 1) / pairs;

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(SdpaBwdParams p, float* 
   const int t = (int)(row % p.Tq);
   const int bh = (int)(row / p.Tq);
   const int b = bh / p.Hq, h = bh % p.Hq;
-  const T* orow = static_cast<const T*>(p.o) + row * p.Dv;
+  const T* orow = static_cast<const T*>(p.o) + b * p.os[0] + h * p.os[1] + t * p.os[2];
   const T* grow = static_cast<const T*>(p.dout) + b * p.dos[0] + h * p.dos[1] + t * p.dos[2];
   float s = 0.f;
   for (int d = lane; d < p.Dv; d += 64) s += to_f32(orow[d]) * to_f32(grow[d]);
@@ -203,6 +203,10 @@ int make_bwd_plan(const mfx_sdpa_bwd_args* a, BwdPlan& out) {
   if (a->mask && a->mask_dtype != MFX_F32 && a->mask_dtype != MFX_BF16 && a->mask_dtype != MFX_F16)
     return fail(MFX_E_UNSUPPORTED, "mask dtype must be f32, bf16 or f16");
   if (!std::isfinite(a->scale)) return fail(MFX_E_INVALID, "scale must be finite");
+  if ((a->fwd_out != nullptr) != (a->fwd_lse != nullptr))
+    return fail(MFX_E_INVALID, "fwd_out and fwd_lse are passed together or not at all");
+  const bool saved = a->fwd_out != nullptr;
+  if (saved && a->fwd_out_strides[3] != 1) return fail(MFX_E_INVALID, "fwd_out feature stride must be 1");
   if (a->D > kMaxD || a->Dv > kMaxD) return fail(MFX_E_UNSUPPORTED, "head size above 256 is not supported");
 
   SdpaBwdParams& p = out.p;
@@ -237,9 +241,18 @@ int make_bwd_plan(const mfx_sdpa_bwd_args* a, BwdPlan& out) {
   p.causal = a->causal ? 1 : 0;
   p.scale = a->scale;
   p.scale_log2 = a->scale * kLog2e;
+  // O: the caller's forward output, or the recomputed one (contiguous, in
+  // the workspace, bound at launch).
+  for (int i = 0; i < 4; ++i)
+    p.os[i] = saved ? a->fwd_out_strides[i]
+                    : (i == 0 ? (int64_t)p.Hq * p.Tq * p.Dv : i == 1 ? (int64_t)p.Tq * p.Dv : i == 2 ? p.Dv : 1);
+  if (saved) {
+    p.o = a->fwd_out;
+    p.lse = a->fwd_lse;
+  }
 
   const int64_t rows = (int64_t)p.B * p.Hq * p.Tq;
-  out.o_bytes = align256((size_t)rows * p.Dv * dtype_size(p.dtype));
+  out.o_bytes = saved ? 0 : align256((size_t)rows * p.Dv * dtype_size(p.dtype));
   out.row_bytes = align256((size_t)rows * sizeof(float));
 
   // The forward pass that regenerates O and lse: the flash kernels where they
@@ -317,17 +330,19 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
   }
   SdpaBwdParams& p = pl.p;
   SdpaParams& f = pl.fwd;
-  f.out = ws;
-  f.lse = reinterpret_cast<float*>(ws + pl.o_bytes);
   float* delta = reinterpret_cast<float*>(ws + pl.o_bytes + pl.row_bytes);
-  p.o = f.out;
-  p.lse = f.lse;
   p.delta = delta;
-
-  if (flash_bf16_supports(f)) rc = launch_flash_bf16(f, s);
-  else if (flash_f32_supports(f)) rc = launch_flash_f32(f, s);
-  else rc = launch_generic(f, s);
-  if (rc != MFX_OK) return rc;
+  if (!args->fwd_out) {
+    // Recompute O and lse into the workspace.
+    f.out = ws;
+    f.lse = reinterpret_cast<float*>(ws + pl.o_bytes);
+    p.o = f.out;
+    p.lse = f.lse;
+    if (flash_bf16_supports(f)) rc = launch_flash_bf16(f, s);
+    else if (flash_f32_supports(f)) rc = launch_flash_f32(f, s);
+    else rc = launch_generic(f, s);
+    if (rc != MFX_OK) return rc;
+  }
 
   if (pl.mfma) return launch_bwd_mfma(p, s);
   const int64_t rows = (int64_t)p.B * p.Hq * p.Tq;

@@ -320,7 +320,7 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
   float dl;
   {
     bf16x8 of[D / 16];
-    load_frags<D>(static_cast<const bf16*>(p.o) + (int64_t)bh * Tq * D, D, qi, Tq, half, of);
+    load_frags<D>(static_cast<const bf16*>(p.o) + b * p.os[0] + h * p.os[1], p.os[2], qi, Tq, half, of);
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
@@ -439,12 +439,14 @@ bool bwd_mfma_supports(const SdpaBwdParams& p) {
   if (p.dtype != MFX_BF16) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (!(p.scale_log2 > 0.f)) return false;
-  const void* ptrs[7] = {p.q, p.k, p.v, p.dout, p.dq, p.dk, p.dv};
+  // p.o is null until launch when O is recomputed (then it is the
+  // workspace: 256-byte aligned, contiguous).
+  const void* ptrs[8] = {p.q, p.k, p.v, p.dout, p.dq, p.dk, p.dv, p.o};
   for (const void* ptr : ptrs)
     if (!aligned16(ptr)) return false;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.dos[i] % 8 || p.dqs[i] % 4 || p.dks[i] % 4 ||
-        p.dvs[i] % 4)
+        p.dvs[i] % 4 || p.os[i] % 8)
       return false;
   // Buffer-resource extents are 31-bit: one kv head's K / V rows, and the
   // query rows (and lse / delta) of all heads of one group.

@@ -37,8 +37,9 @@ struct SdpaParams {
 };
 
 // Backward pass (mfx_sdpa_bwd).  o / lse come from the recomputed forward
-// pass: o contiguous [B][Hq][Tq][Dv] of `dtype`, lse and delta
-// [B][Hq][Tq] fp32 (log2 units for lse; delta = rowsum(dO * o)).
+// pass or from the caller's forward call: o [B][Hq][Tq][Dv] of `dtype` at
+// element strides os (feature stride 1), lse and delta [B][Hq][Tq] fp32
+// (log2 units for lse; delta = rowsum(dO * o)).
 struct SdpaBwdParams {
   const void* q;
   const void* k;
@@ -51,7 +52,7 @@ struct SdpaBwdParams {
   void* dv;
   const float* lse;
   float* delta;  // written by the delta pass or by the matrix-core dQ kernel
-  int64_t qs[4], ks[4], vs[4], dos[4], dqs[4], dks[4], dvs[4], ms[4];
+  int64_t qs[4], ks[4], vs[4], dos[4], dqs[4], dks[4], dvs[4], ms[4], os[4];
   int B, Hq, Hkv, Tq, Tk, D, Dv;
   int group;
   int mask_dtype;

@@ -198,6 +198,22 @@ class Planner {
   };
   std::map<size_t, GemmMeta> gemm_meta_;
   std::map<size_t, EwMeta> ew_meta_;
+  // Launch arguments of SDPA forward / backward steps (by step index), for
+  // the pass that hands a forward's output and row log-sum-exp to the
+  // backward of the same attention.
+  struct SdpaMeta {
+    mfx_sdpa_args a;
+    int q, k, v, out_v, mask, wq, ws_v;
+    size_t ws;
+    int64_t qo, ko, vo, mo;
+  };
+  struct SdpaBwdMeta {
+    mfx_sdpa_bwd_args a;
+    int q, k, v, g, dq, dk, dv, ws_v;
+    size_t ws;
+  };
+  std::map<size_t, SdpaMeta> sdpa_meta_;
+  std::map<size_t, SdpaBwdMeta> sdpa_bwd_meta_;
   std::vector<Type> temp_types_;
   std::vector<int64_t> temp_bytes_;
   std::shared_ptr<std::vector<Loc>> loc_ = std::make_shared<std::vector<Loc>>();
@@ -1045,32 +1061,44 @@ class Planner {
     wt.dtype = DType::kU8;
     wt.dims = {(int64_t)ws};
     const int ws_v = new_temp(wt);
-    const int q = n.in[0], k = n.in[1], v = n.in[2], g = n.in[3];
-    const int dq = n.out[0], dk = n.out[1], dv = n.out[2];
+    const SdpaBwdMeta m{a, n.in[0], n.in[1], n.in[2], n.in[3], n.out[0], n.out[1], n.out[2], ws_v, ws};
+    sdpa_bwd_meta_[plan_.steps_.size()] = m;
+    plan_.steps_.push_back(sdpa_bwd_step(m, -1, -1));
+    io_.push_back(StepIO{{m.q, m.k, m.v, m.g}, {m.dq, m.dk, m.dv, m.ws_v}});
+  }
+
+  // The backward step; with fwd_out >= 0 it reads that forward output and
+  // the row log-sum-exp in value lse instead of recomputing them.
+  Step sdpa_bwd_step(const SdpaBwdMeta& m, int fwd_out, int lse) {
     auto loc = loc_;
     Plan* plan = &plan_;
+    const mfx_sdpa_bwd_args& a = m.a;
+    const double B = a.B, N = a.Hq, T = a.Tq, S = a.Tk, H = a.D, Hv = a.Dv;
     Step s;
     s.kind = "sdpa_bwd";
-    s.label = "mfx.sdpa_bwd";
-    // recomputed forward (2 products) + backward (dP, dV, dK, and S, dP, dQ)
-    s.flops = 2.0 * B * N * (double)T * S * (2 * H + 2 * Hv + 2 * H + Hv + H + Hv);
-    s.run = [a, q, k, v, g, dq, dk, dv, ws_v, ws, loc, plan](const ExecBuffers& b, std::string& err) {
-      mfx_sdpa_bwd_args r = a;
-      r.q = plan->ptr((*loc)[q], b);
-      r.k = plan->ptr((*loc)[k], b);
-      r.v = plan->ptr((*loc)[v], b);
-      r.dout = plan->ptr((*loc)[g], b);
-      r.dq = plan->ptr((*loc)[dq], b);
-      r.dk = plan->ptr((*loc)[dk], b);
-      r.dv = plan->ptr((*loc)[dv], b);
-      r.workspace = plan->ptr((*loc)[ws_v], b);
-      r.workspace_bytes = ws;
+    s.label = fwd_out >= 0 ? "mfx.sdpa_bwd (forward's out and lse)" : "mfx.sdpa_bwd";
+    // backward (S, dP, dV, dK, and S, dP, dQ), plus the recomputed forward (S, PV)
+    s.flops = 2.0 * B * N * T * S * (4 * H + 3 * Hv) + (fwd_out >= 0 ? 0.0 : 2.0 * B * N * T * S * (H + Hv));
+    s.run = [m, fwd_out, lse, loc, plan](const ExecBuffers& b, std::string& err) {
+      mfx_sdpa_bwd_args r = m.a;
+      r.q = plan->ptr((*loc)[m.q], b);
+      r.k = plan->ptr((*loc)[m.k], b);
+      r.v = plan->ptr((*loc)[m.v], b);
+      r.dout = plan->ptr((*loc)[m.g], b);
+      r.dq = plan->ptr((*loc)[m.dq], b);
+      r.dk = plan->ptr((*loc)[m.dk], b);
+      r.dv = plan->ptr((*loc)[m.dv], b);
+      r.workspace = plan->ptr((*loc)[m.ws_v], b);
+      r.workspace_bytes = m.ws;
+      if (fwd_out >= 0) {
+        r.fwd_out = plan->ptr((*loc)[fwd_out], b);
+        r.fwd_lse = static_cast<const float*>(plan->ptr((*loc)[lse], b));
+      }
       int rc = mfx_sdpa_bwd(&r, b.stream);
       if (rc != MFX_OK) err = mfx_last_error();
       return rc;
     };
-    plan_.steps_.push_back(std::move(s));
-    io_.push_back(StepIO{{q, k, v, g}, {dq, dk, dv, ws_v}});
+    return s;
   }
 
   void emit_sdpa(const Node& n) {
@@ -1188,38 +1216,103 @@ class Planner {
                    std::vector<int64_t>(a.mask_strides, a.mask_strides + 4));
     if (wq >= 0) check_dense("sdpa q-norm weight", wq, a.D);
     const int eb = dtype_bytes(dt);
-    const int64_t qo = offs[0] * eb, ko = offs[1] * eb, vo = offs[2] * eb;
     const int64_t mo = moff * (mask >= 0 ? dtype_bytes(ty(mask).dtype) : 0);
-    auto loc = loc_;
-    Plan* plan = &plan_;
-    Step s;
-    s.kind = "sdpa";
-    s.label = a.causal ? "sdpa causal" : "sdpa";
-    double keys = a.causal ? (double)a.Tq * (a.Tq + 1) / 2.0 : (double)a.Tq * a.Tk;
-    s.flops = 2.0 * a.B * a.Hq * keys * (a.D + a.Dv);
-    s.run = [a, q, k, v, out_v, mask, wq, ws_v, ws, qo, ko, vo, mo, loc, plan](const ExecBuffers& b,
-                                                                               std::string& err) {
-      mfx_sdpa_args r = a;
-      r.q = (char*)plan->ptr((*loc)[q], b) + qo;
-      r.k = (char*)plan->ptr((*loc)[k], b) + ko;
-      r.v = (char*)plan->ptr((*loc)[v], b) + vo;
-      r.out = plan->ptr((*loc)[out_v], b);
-      r.mask = mask >= 0 ? (char*)plan->ptr((*loc)[mask], b) + mo : nullptr;
-      r.q_rms_weight = wq >= 0 ? plan->ptr((*loc)[wq], b) : nullptr;
-      if (ws_v >= 0) {
-        r.workspace = plan->ptr((*loc)[ws_v], b);
-        r.workspace_bytes = ws;
-      }
-      int rc = mfx_sdpa_fwd(&r, b.stream);
-      if (rc != MFX_OK) err = mfx_last_error();
-      return rc;
-    };
-    plan_.steps_.push_back(std::move(s));
+    const SdpaMeta m{a, q, k, v, out_v, mask, wq, ws_v, ws, offs[0] * eb, offs[1] * eb, offs[2] * eb, mo};
+    sdpa_meta_[plan_.steps_.size()] = m;
+    plan_.steps_.push_back(sdpa_step(m, -1));
     StepIO io{{q, k, v}, {out_v}};
     if (mask >= 0) io.reads.push_back(mask);
     if (wq >= 0) io.reads.push_back(wq);
     if (ws_v >= 0) io.writes.push_back(ws_v);
     io_.push_back(io);
+  }
+
+  // The forward step; with lse >= 0 it also writes the row log-sum-exp there.
+  Step sdpa_step(const SdpaMeta& m, int lse) {
+    auto loc = loc_;
+    Plan* plan = &plan_;
+    const mfx_sdpa_args& a = m.a;
+    Step s;
+    s.kind = "sdpa";
+    s.label = std::string(a.causal ? "sdpa causal" : "sdpa") + (lse >= 0 ? " (+ lse)" : "");
+    double keys = a.causal ? (double)a.Tq * (a.Tq + 1) / 2.0 : (double)a.Tq * a.Tk;
+    s.flops = 2.0 * a.B * a.Hq * keys * (a.D + a.Dv);
+    s.run = [m, lse, loc, plan](const ExecBuffers& b, std::string& err) {
+      mfx_sdpa_args r = m.a;
+      r.q = (char*)plan->ptr((*loc)[m.q], b) + m.qo;
+      r.k = (char*)plan->ptr((*loc)[m.k], b) + m.ko;
+      r.v = (char*)plan->ptr((*loc)[m.v], b) + m.vo;
+      r.out = plan->ptr((*loc)[m.out_v], b);
+      r.mask = m.mask >= 0 ? (char*)plan->ptr((*loc)[m.mask], b) + m.mo : nullptr;
+      r.q_rms_weight = m.wq >= 0 ? plan->ptr((*loc)[m.wq], b) : nullptr;
+      if (m.ws_v >= 0) {
+        r.workspace = plan->ptr((*loc)[m.ws_v], b);
+        r.workspace_bytes = m.ws;
+      }
+      if (lse >= 0) r.lse = static_cast<float*>(plan->ptr((*loc)[lse], b));
+      int rc = mfx_sdpa_fwd(&r, b.stream);
+      if (rc != MFX_OK) err = mfx_last_error();
+      return rc;
+    };
+    return s;
+  }
+
+  // A backward step whose q, k and v are the operands of an earlier forward
+  // step with the same shape, scale and no mask, causal limit or q RMSNorm
+  // (a training step's attention and its gradient): the forward also writes
+  // its row log-sum-exp, and the backward reads it and the forward's output
+  // instead of recomputing both (same forward kernel, so the same bits).
+  void link_sdpa_backward() {
+    for (auto& bw : sdpa_bwd_meta_) {
+      const SdpaBwdMeta& m = bw.second;
+      const mfx_sdpa_bwd_args& ba = m.a;
+      if (ba.mask || ba.causal) continue;
+      for (auto& fw : sdpa_meta_) {
+        if (fw.first >= bw.first) break;
+        const SdpaMeta& f = fw.second;
+        const mfx_sdpa_args& fa = f.a;
+        if (resolve_alias(f.q) != resolve_alias(m.q) || resolve_alias(f.k) != resolve_alias(m.k) ||
+            resolve_alias(f.v) != resolve_alias(m.v))
+          continue;
+        if (f.qo || f.ko || f.vo || f.mask >= 0 || fa.causal || fa.q_rms_eps >= 0.f || f.wq >= 0) continue;
+        if (fa.B != ba.B || fa.Hq != ba.Hq || fa.Hkv != ba.Hkv || fa.Tq != ba.Tq || fa.Tk != ba.Tk || fa.D != ba.D ||
+            fa.Dv != ba.Dv || fa.scale != ba.scale || fa.dtype != ba.dtype)
+          continue;
+        bool same = true;
+        for (int i = 0; i < 4; ++i)
+          same = same && fa.q_strides[i] == ba.q_strides[i] && fa.k_strides[i] == ba.k_strides[i] &&
+                 fa.v_strides[i] == ba.v_strides[i];
+        if (!same) continue;
+        // Backward workspace without the recomputed output.
+        mfx_sdpa_bwd_args probe = ba;
+        probe.q = probe.k = probe.v = probe.dout = (void*)0x10000;
+        probe.dq = probe.dk = probe.dv = (void*)0x10000;
+        probe.fwd_out = (void*)0x10000;
+        probe.fwd_lse = (const float*)0x10000;
+        for (int i = 0; i < 4; ++i) probe.fwd_out_strides[i] = fa.o_strides[i];
+        const size_t ws = mfx_sdpa_bwd_workspace_size(&probe);
+        if (!ws) continue;
+        Type lt;
+        lt.dtype = DType::kF32;
+        lt.dims = {fa.B * fa.Hq * fa.Tq};
+        const int lse = new_temp(lt);
+        Type wt;
+        wt.dtype = DType::kU8;
+        wt.dims = {(int64_t)ws};
+        SdpaBwdMeta mb = m;
+        mb.a.fwd_out_strides[0] = fa.o_strides[0];
+        mb.a.fwd_out_strides[1] = fa.o_strides[1];
+        mb.a.fwd_out_strides[2] = fa.o_strides[2];
+        mb.a.fwd_out_strides[3] = fa.o_strides[3];
+        mb.ws_v = new_temp(wt);
+        mb.ws = ws;
+        plan_.steps_[fw.first] = sdpa_step(f, lse);
+        io_[fw.first].writes.push_back(lse);
+        plan_.steps_[bw.first] = sdpa_bwd_step(mb, f.out_v, lse);
+        io_[bw.first] = StepIO{{mb.q, mb.k, mb.v, mb.g, f.out_v, lse}, {mb.dq, mb.dk, mb.dv, mb.ws_v}};
+        break;
+      }
+    }
   }
 
   void emit_concat(const Node& n) {
@@ -1271,6 +1364,8 @@ class Planner {
     io_.clear();
     gemm_meta_.clear();
     ew_meta_.clear();
+    sdpa_meta_.clear();
+    sdpa_bwd_meta_.clear();
     temp_types_.clear();
     temp_bytes_.clear();
     flat_alias_.clear();
@@ -1316,6 +1411,7 @@ class Planner {
       }
       seen.insert(v);
     }
+    link_sdpa_backward();  // rewrites steps in place: before the pass that merges steps
     fuse_gemm_epilogues();
   }
 

@@ -94,6 +94,7 @@ class SdpaArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("mask_dtype", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("lse", ctypes.c_void_p),
     ]
 
 
@@ -128,6 +129,9 @@ class SdpaBwdArgs(ctypes.Structure):
         ("causal", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("mask_dtype", ctypes.c_int32),
+        ("fwd_out", ctypes.c_void_p),
+        ("fwd_lse", ctypes.c_void_p),
+        ("fwd_out_strides", I64x4),
     ]
 
 
@@ -426,7 +430,7 @@ def _dims(t, layout):
 
 
 def sdpa_args(q, k, v, out, *, scale=None, causal=False, mask=None, layout="bhtd",
-              q_rms_eps=None, q_rms_weight=None, workspace=None) -> SdpaArgs:
+              q_rms_eps=None, q_rms_weight=None, workspace=None, lse=None) -> SdpaArgs:
     B, Hq, Tq, D = _dims(q, layout)
     _, Hkv, Tk, _ = _dims(k, layout)
     Dv = v.shape[-1]
@@ -458,14 +462,20 @@ def sdpa_args(q, k, v, out, *, scale=None, causal=False, mask=None, layout="bhtd
     if workspace is not None:
         a.workspace = workspace.data_ptr()
         a.workspace_bytes = workspace.numel() * workspace.element_size()
+    if lse is not None:
+        if lse.dtype != _torch().float32 or lse.numel() != B * Hq * Tq or not lse.is_contiguous():
+            raise ValueError("lse must be a contiguous f32 tensor of B * Hq * Tq elements")
+        a.lse = lse.data_ptr()
     return a
 
 
 def sdpa(q, k, v, *, scale=None, causal=False, mask=None, layout="bhtd", q_rms_eps=None,
-         q_rms_weight=None, out=None, workspace=None):
+         q_rms_weight=None, out=None, workspace=None, lse=None):
     """softmax(scale * Q K^T + mask) V (mfx_sdpa_fwd).
 
     layout "bhtd": q [B,Hq,Tq,D], k/v [B,Hkv,Tk,D]; "bthd": JAX's BTNH layout.
+    lse: optional f32 [B * Hq * Tq] output of the row log-sum-exp (log2
+    units), for sdpa_bwd(fwd_out=..., fwd_lse=...).
     """
     torch = _torch()
     _require_gpu(q, k, v, mask, q_rms_weight)
@@ -474,7 +484,7 @@ def sdpa(q, k, v, *, scale=None, causal=False, mask=None, layout="bhtd", q_rms_e
         shape[-1] = v.shape[-1]
         out = torch.empty(shape, dtype=q.dtype, device=q.device)
     a = sdpa_args(q, k, v, out, scale=scale, causal=causal, mask=mask, layout=layout,
-                  q_rms_eps=q_rms_eps, q_rms_weight=q_rms_weight, workspace=workspace)
+                  q_rms_eps=q_rms_eps, q_rms_weight=q_rms_weight, workspace=workspace, lse=lse)
     check(load().mfx_sdpa_fwd(ctypes.byref(a), ctypes.c_void_p(_stream_handle(q))))
     return out
 
@@ -512,7 +522,7 @@ def sdpa_kernel_name(q, k, v, **kw) -> str:
 
 
 def sdpa_bwd_args(q, k, v, dout, dq, dk, dv, *, scale=None, causal=False, mask=None, layout="bhtd",
-                  workspace=None) -> SdpaBwdArgs:
+                  workspace=None, fwd_out=None, fwd_lse=None) -> SdpaBwdArgs:
     B, Hq, Tq, D = _dims(q, layout)
     _, Hkv, Tk, _ = _dims(k, layout)
     Dv = v.shape[-1]
@@ -539,17 +549,25 @@ def sdpa_bwd_args(q, k, v, dout, dq, dk, dv, *, scale=None, causal=False, mask=N
     if workspace is not None:
         a.workspace = workspace.data_ptr()
         a.workspace_bytes = workspace.numel() * workspace.element_size()
+    if fwd_out is not None:
+        a.fwd_out = fwd_out.data_ptr()
+        a.fwd_out_strides = I64x4(*_strides4(fwd_out, layout))
+    if fwd_lse is not None:
+        a.fwd_lse = fwd_lse.data_ptr()
     return a
 
 
-def sdpa_bwd(q, k, v, dout, *, scale=None, causal=False, mask=None, layout="bhtd", workspace=None):
+def sdpa_bwd(q, k, v, dout, *, scale=None, causal=False, mask=None, layout="bhtd", workspace=None,
+             fwd_out=None, fwd_lse=None):
     """(dq, dk, dv) of softmax(scale * Q K^T + mask) V for upstream gradient dout
-    (mfx_sdpa_bwd); layouts as sdpa()."""
+    (mfx_sdpa_bwd); layouts as sdpa().  fwd_out / fwd_lse: the forward call's
+    output and lse on the same inputs (both or neither) to skip the
+    recomputed forward pass."""
     torch = _torch()
-    _require_gpu(q, k, v, dout, mask)
+    _require_gpu(q, k, v, dout, mask, fwd_out, fwd_lse)
     dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
     a = sdpa_bwd_args(q, k, v, dout, dq, dk, dv, scale=scale, causal=causal, mask=mask, layout=layout,
-                      workspace=workspace)
+                      workspace=workspace, fwd_out=fwd_out, fwd_lse=fwd_lse)
     check(load().mfx_sdpa_bwd(ctypes.byref(a), ctypes.c_void_p(_stream_handle(q))))
     return dq, dk, dv
 

@@ -697,3 +697,54 @@ def test_tanh_device_accuracy_and_paths(cuda):
     assert np.isnan(y[np.isnan(x)]).all()
     assert (y[x == np.inf] == 1).all() and (y[x == -np.inf] == -1).all()
     assert np.signbit(y[(x == 0) & np.signbit(x)]).all()
+
+
+# ---------------------------------------------------------------- backward from forward residuals
+
+@pytest.mark.parametrize("dt,shape,causal,layout,group", [
+    ("bf16", (2, 4, 256, 128), True, "bhtd", 1),   # matrix-core backward, causal
+    ("bf16", (2, 4, 192, 64), False, "bthd", 2),   # BTNH (strided O), GQA, d = 64
+    ("f32", (2, 2, 100, 64), False, "bhtd", 1),    # f32: flash forward, generic backward
+])
+def test_sdpa_bwd_from_forward_residuals(cuda, dt, shape, causal, layout, group):
+    """mfx_sdpa_bwd given the forward call's output and lse (mfx_sdpa_fwd's
+    lse output) skips its recompute and returns the recomputing call's
+    gradients bit for bit; the lse itself matches fp64 log2-sum-exp2 of the
+    scaled, causally limited scores -- within 1e-4 for f32, and for bf16
+    within 2^-9 / ln 2 = 0.0028 (the bf16 kernels sum the bf16-rounded
+    probabilities that also form O, each within 2^-9 relative)."""
+    import numpy as np
+
+    from jax_mlx_amd import native as nt
+
+    torch = cuda
+    B, H, T, D = shape
+    Hkv = H // group
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    g = torch.Generator(device="cpu").manual_seed(sum(shape) + group)
+
+    def mk(heads):
+        t = torch.randn(B, heads, T, D, generator=g)
+        if layout == "bthd":
+            t = t.transpose(1, 2).contiguous()
+        return t.to(tdt).cuda()
+
+    q, k, v, go = mk(H), mk(Hkv), mk(Hkv), mk(H)
+    lse = torch.empty(B * H * T, dtype=torch.float32, device="cuda")
+    out = nt.sdpa(q, k, v, causal=causal, layout=layout, lse=lse)
+    ref = nt.sdpa_bwd(q, k, v, go, causal=causal, layout=layout)
+    got = nt.sdpa_bwd(q, k, v, go, causal=causal, layout=layout, fwd_out=out, fwd_lse=lse)
+    torch.cuda.synchronize()
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    # lse against fp64 (log2 units, scale 1/sqrt(D))
+    qh = (q if layout == "bhtd" else q.transpose(1, 2)).double().cpu().numpy()
+    kh = (k if layout == "bhtd" else k.transpose(1, 2)).double().cpu().numpy()
+    kh = np.repeat(kh, group, axis=1)
+    s = np.einsum("bhtd,bhsd->bhts", qh, kh) / np.sqrt(D)
+    if causal:
+        s = np.where(np.tril(np.ones((T, T), dtype=bool)), s, -np.inf)
+    m = s.max(-1, keepdims=True)
+    want = (m[..., 0] + np.log(np.exp(s - m).sum(-1))) / np.log(2.0)
+    err = np.abs(lse.cpu().numpy().reshape(B, H, T) - want).max()
+    assert err <= (2.0 ** -9 / np.log(2.0) if dt == "bf16" else 1e-4), err

@@ -411,6 +411,19 @@ def test_transformer_plan(api):
     assert sd["i:offsets"] == [0, 128, 256, 0]  # q, k, v read in place from the QKV projection
 
 
+def test_sdpa_vjp_links_forward_and_backward(api):
+    """jax.vjp of mlx_dot_product_attention in one module: the forward step
+    also writes its row log-sum-exp and the backward reads it and the
+    forward's output instead of recomputing them; a backward on another q
+    value keeps its recompute."""
+    d = api.inspect(M.sdpa_vjp_module())
+    assert [s["label"] for s in d["plan"]["steps"]] == ["sdpa (+ lse)", "mfx.sdpa_bwd (forward's out and lse)"]
+    d2 = api.inspect(M.sdpa_vjp_module(same_inputs=False))
+    assert [s["label"] for s in d2["plan"]["steps"]] == ["sdpa", "mfx.sdpa_bwd"]
+    # the recomputed output no longer needs workspace in the arena
+    assert d["plan"]["arena_bytes"] < d2["plan"]["arena_bytes"]
+
+
 @pytest.mark.parametrize("epilogue", ["bias", "bias_gelu", "bias_residual"])
 def test_dense_epilogue_fuses_into_gemm(api, epilogue):
     """A dot_general whose only reader is one elementwise program at the

@@ -494,6 +494,24 @@ def test_dense_epilogue_unaligned_weights_fall_back(client):
     assert np.abs(outs[0] - outs[1]).max() <= 1e-5
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_sdpa_vjp_module_linked(client, dt):
+    """jax.vjp of mlx_dot_product_attention as one module: the plan hands the
+    forward's output and lse to the backward (no recompute).  Every result
+    equals the same module with the backward on a separate (equal) q
+    argument, which the planner does not link and which recomputes."""
+    rng = np.random.default_rng(41)
+    B, T, N, H = 2, 128, 4, 64
+    q, k, v, g = (rng.standard_normal((B, T, N, H)).astype(np.float32) for _ in range(4))
+    if dt == "bf16":
+        q, k, v, g = (bf16_round(a) for a in (q, k, v, g))
+    linked = run(client, M.sdpa_vjp_module(B=B, T=T, N=N, H=H, dt=dt), [q, k, v, g], [dt] * 4)
+    plain = run(client, M.sdpa_vjp_module(B=B, T=T, N=N, H=H, dt=dt, same_inputs=False), [q, k, v, g, q],
+                [dt] * 5)
+    for a, b in zip(linked, plain):
+        assert np.array_equal(a, b)
+
+
 def test_escaping_intermediates_layer_norm(client, oracle):
     """Escape guard (reference src/jax_mlx_pjrt.cpp:1843-1855): a LayerNorm
     whose mean and variance are also results.  The fusion fires and the
