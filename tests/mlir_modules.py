@@ -645,6 +645,22 @@ def dense_module(M=256, K=128, N=192, epilogue="bias", dt="f32", escape=None):
     return module("jit_dense", [f.text(outs, [ty(ys, dt)] * len(outs))])
 
 
+def batched_dense_module(Bt=3, M=100, K=64, N=96, dt="f32"):
+    """A batched product 'bmk,bkn->bmn' (batching dims 0 x 0) followed by a
+    bias add and a tanh GELU over its [Bt, M, N] result.  Arguments:
+    x [Bt, M, K], w [Bt, K, N], b [N]."""
+    f = Fn("main", [([Bt, M, K], dt), ([Bt, K, N], dt), ([N], dt)])
+    y, ys = f.dot_general(f.arg(0), f.arg(1), [Bt, M, K], [Bt, K, N], ([0], [0]), ([2], [1]), dt)
+    u = f.binary("add", y, f.bcast(f.arg(2), [N], [2], ys, dt), ys, dt)
+    x3 = f.binary("multiply", f.binary("multiply", u, u, ys, dt), u, ys, dt)
+    inner = f.binary("add", u, f.binary("multiply", f.splat(0.044715, ys, dt), x3, ys, dt), ys, dt)
+    inner = f.binary("multiply", f.splat(math.sqrt(2.0 / math.pi), ys, dt), inner, ys, dt)
+    t = f.unary("tanh", inner, ys, dt)
+    g = f.binary("multiply", f.binary("multiply", f.splat(0.5, ys, dt), u, ys, dt),
+                 f.binary("add", f.splat(1.0, ys, dt), t, ys, dt), ys, dt)
+    return module("jit_batched_dense", [f.text([g], [ty(ys, dt)])])
+
+
 def config4_inputs(seed=4, layers=4, B=32, T=256, d=512, mlp=2048):
     """Arguments of transformer_module in order, as BASELINE config 4 states
     them: x ~ N(0,1), Xavier-uniform weights (U(+-sqrt(6 / (fan_in +

@@ -440,6 +440,12 @@ def test_dense_epilogue_not_fused_when_product_escapes(api, escape):
     assert s[0] == "gemm" and "gemm_ew" not in s and s.count("elementwise") >= 1
 
 
+def test_batched_dense_epilogue_fuses(api):
+    """A batched dot_general ('bmk,bkn->bmn') with its bias + GELU consumer:
+    one fused launch over batch * M rows."""
+    assert steps(api.inspect(M.batched_dense_module())) == ["gemm_ew"]
+
+
 def test_dense_epilogue_rules(api):
     """Products the f32 tile kernel does not take keep two steps: bf16
     operands, K not a multiple of 4, odd N."""

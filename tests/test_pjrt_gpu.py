@@ -467,6 +467,19 @@ def test_dense_epilogue_fused(client, epilogue):
     assert np.abs(y - ref).max() <= 2e-5
 
 
+def test_batched_dense_epilogue(client):
+    """Batched dense layer + bias + tanh GELU through PJRT (one fused launch),
+    against fp64.  Bar 2e-5 max-abs (O(1) outputs)."""
+    rng = np.random.default_rng(33)
+    x = rng.standard_normal((3, 100, 64)).astype(np.float32)
+    w = (rng.standard_normal((3, 64, 96)) / 8.0).astype(np.float32)
+    b = (0.5 * rng.standard_normal(96)).astype(np.float32)
+    (y,) = run(client, M.batched_dense_module(), [x, w, b], ["f32"] * 3)
+    u = np.einsum("bmk,bkn->bmn", x.astype(np.float64), w.astype(np.float64)) + b
+    ref = 0.5 * u * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (u + 0.044715 * u ** 3)))
+    assert np.abs(y - ref).max() <= 2e-5
+
+
 def test_dense_epilogue_unaligned_weights_fall_back(client):
     """Weights passed as a device view 4 bytes off 16-byte alignment: the
     fused kernel does not take them, so the step runs the GEMM into its
