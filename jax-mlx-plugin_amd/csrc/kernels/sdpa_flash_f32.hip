@@ -38,21 +38,41 @@ bool flash_f32_use_split(const SdpaParams& p) {
 
 namespace {
 
+// Bytes from the first to the last valid element of `rows` rows of D floats
+// at `stride` floats apart (0 when no row is valid).
 template <int D>
+__device__ __forceinline__ int rows_extent(int rows, int64_t stride) {
+  return rows > 0 ? (int)(((int64_t)(rows - 1) * stride + D) * 4) : 0;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const float* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ f32x4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <int D, bool MASK>
 struct Cfg {
   static constexpr int KROW = D + 4;               // floats per K row (16 B pad)
   static constexpr int VROW = D + 8;               // floats per V row (32 B pad)
   static constexpr int DCH = D / 4;                // 16-byte chunks per row
-  static constexpr int CH = kBN * DCH / kNT;       // chunks per thread per tile
+  // Keys per LDS stage: two 32-key sub-tiles per barrier at D = 64 without
+  // a mask (70 KB of LDS per workgroup, two workgroups per CU), one
+  // otherwise (the masked kernel's extra state would spill).
+  static constexpr int KS = (D == 64 && !MASK) ? 64 : 32;
+  static constexpr int NSUB = KS / kBN;
+  static constexpr int CH = KS * DCH / kNT;        // chunks per thread per stage
 };
 
 // Two workgroups per CU (256 VGPRs) except masked D = 128, whose extra mask
 // state would spill at that bound.
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(kNT, (D == 128 && MASK) ? 1 : 2) void flash_f32_kernel(SdpaParams p) {
-  using C = Cfg<D>;
-  __shared__ __attribute__((aligned(16))) float k_lds[2][kBN * C::KROW];
-  __shared__ __attribute__((aligned(16))) float v_lds[2][kBN * C::VROW];
+  using C = Cfg<D, MASK>;
+  __shared__ __attribute__((aligned(16))) float k_lds[2][C::KS * C::KROW];
+  __shared__ __attribute__((aligned(16))) float v_lds[2][C::KS * C::VROW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,6 +103,12 @@ __global__ __launch_bounds__(kNT, (D == 128 && MASK) ? 1 : 2) void flash_f32_ker
   const int q0 = mblk * kBM + wave * 32;
   const int qi = q0 + l32;
 
+  // The exponent scale enters as |scale_log2| with its sign folded into Q
+  // (negating Q negates every score exactly), so a row's largest scaled
+  // score is |scale_log2| times its largest raw score.
+  const float sl2 = fabsf(p.scale_log2);
+  const float qsign = p.scale_log2 < 0.f ? -1.f : 1.f;
+
   // qf[c*4+e] = Q[qi][c*8 + half*4 + e]: the k-slot (half) of MFMA step
   // (c, e) is feature c*8 + half*4 + e, matched by the K reads below.
   float qf[D / 2];
@@ -93,28 +119,37 @@ __global__ __launch_bounds__(kNT, (D == 128 && MASK) ? 1 : 2) void flash_f32_ker
       f32x4 t = *reinterpret_cast<const f32x4*>(qrow + c * 8);
       if (qi >= Tq) t = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qf[c * 4 + e] = t[e];
+      for (int e = 0; e < 4; ++e) qf[c * 4 + e] = t[e] * qsign;
     }
   }
 
   int kv_end = Tk;
   if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kBM));
-  const int ntiles = (kv_end + kBN - 1) / kBN;
+  const int nstages = (kv_end + C::KS - 1) / C::KS;
 
+  // K/V stages come through buffer resources spanning exactly the stage's
+  // valid rows: rows past Tk read as zero (sequence stride >= D) or as
+  // valid rows (overlapping rows), whose scores are masked either way.
+  // Every lane's byte offsets are fixed for the whole kernel; the stage
+  // moves the resource base.
+  int koff[C::CH], voff[C::CH];
+#pragma unroll
+  for (int i = 0; i < C::CH; ++i) {
+    const int c = tid + i * kNT;
+    const int row = c / C::DCH, col = c % C::DCH;
+    koff[i] = (int)((row * ks2 + col * 4) * 4);
+    voff[i] = (int)((row * vs2 + col * 4) * 4);
+  }
   f32x4 kreg[C::CH], vreg[C::CH];
-  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  auto gload = [&](int t) {
-    const int kb = t * kBN;
+  auto gload = [&](int st) {
+    const int kb = st * C::KS;
+    const int rows = min(C::KS, Tk - kb);
+    const auto rk = f32_rsrc(kp + (int64_t)kb * ks2, rows_extent<D>(rows, ks2));
+    const auto rv = f32_rsrc(vp + (int64_t)kb * vs2, rows_extent<D>(rows, vs2));
 #pragma unroll
     for (int i = 0; i < C::CH; ++i) {
-      const int c = tid + i * kNT;
-      const int row = c / C::DCH, col = c % C::DCH;
-      const int key = kb + row;
-      const int64_t kr = (int64_t)min(key, Tk - 1);
-      f32x4 a = *reinterpret_cast<const f32x4*>(kp + kr * ks2 + col * 4);
-      f32x4 v = *reinterpret_cast<const f32x4*>(vp + kr * vs2 + col * 4);
-      kreg[i] = key < Tk ? a : zero4;
-      vreg[i] = key < Tk ? v : zero4;
+      kreg[i] = ld4(rk, koff[i]);
+      vreg[i] = ld4(rv, voff[i]);
     }
   };
   auto lstore = [&](int buf) {
@@ -132,71 +167,106 @@ __global__ __launch_bounds__(kNT, (D == 128 && MASK) ? 1 : 2) void flash_f32_ker
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  // m_run: the exponent base of a row (log2 units), which trails the row's
+  // running maximum by at most kSlack, so every exp2 is at most 2^kSlack.
+  // O and l are rescaled only when some row's maximum passes its base by
+  // more than that (a wavefront-uniform branch, rare after the first tile).
+  constexpr float kSlack = 8.f;
   float m_run = -INFINITY, l_run = 0.f;
-  const float sl2 = p.scale_log2;
 
-  if (ntiles > 0) {
+  if (nstages > 0) {
     gload(0);
     lstore(0);
   }
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-    const int kb = t * kBN;
-    const bool active = (q0 < Tq) && (!CAUSAL || kb <= q0 + 31);
-    if (active) {
-      f32x16 s;
+  for (int st = 0; st < nstages; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nstages) gload(st + 1);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    for (int u = 0; u < C::NSUB; ++u) {
+      const int kb = st * C::KS + u * kBN;
+      const float* kt = &k_lds[buf][u * kBN * C::KROW];
+      const float* vt = &v_lds[buf][u * kBN * C::VROW];
+      const bool active = kb < kv_end && (q0 < Tq) && (!CAUSAL || kb <= q0 + 31);
+      if (active) {
+        f32x16 s;
 #pragma unroll
-      for (int c = 0; c < D / 8; ++c) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(&k_lds[buf][l32 * C::KROW + c * 8 + half * 4]);
+        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+        __builtin_amdgcn_s_setprio(3);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          s = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[c * 4 + e], s, 0, 0, 0);
-      }
-      const bool edge = (kb + kBN > Tk) || (CAUSAL && kb + kBN - 1 > q0);
-      float mx = -INFINITY;
+        for (int c = 0; c < D / 8; ++c) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(&kt[l32 * C::KROW + c * 8 + half * 4]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = s[i] * sl2;
-        const int key = kb + (i >> 2) * 8 + half * 4 + (i & 3);
-        if constexpr (MASK) {
-          if (qi < Tq && key < Tk)
-            x += mask_log2(load_mask(p.mask, p.mask_dtype,
-                                    b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]));
+          for (int e = 0; e < 4; ++e)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[c * 4 + e], s, 0, 0, 0);
         }
-        if (edge && (key >= Tk || (CAUSAL && key > qi))) x = -INFINITY;
-        s[i] = x;
-        mx = fmaxf(mx, x);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float base = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - base);
-      m_run = m_new;
-      l_run *= alpha;
+        __builtin_amdgcn_s_setprio(0);
+        // Tiles with masked keys (additive mask, past Tk, causal diagonal)
+        // form the scaled scores one by one; the others keep the raw scores
+        // and fold the scale into the exponent's fma.
+        const bool scaled = MASK || (kb + kBN > Tk) || (CAUSAL && kb + kBN - 1 > q0);
+        float mx;
+        if (scaled) {
+          mx = -INFINITY;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+          for (int i = 0; i < 16; ++i) {
+            float x = s[i] * sl2;
+            const int key = kb + (i >> 2) * 8 + half * 4 + (i & 3);
+            if constexpr (MASK) {
+              if (qi < Tq && key < Tk)
+                x += mask_log2(load_mask(p.mask, p.mask_dtype,
+                                        b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]));
+            }
+            if (key >= Tk || (CAUSAL && key > qi)) x = -INFINITY;
+            s[i] = x;
+            mx = fmaxf(mx, x);
+          }
+        } else {
+          float r = s[0];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[i] = exp2f(s[i] - base);
-        l_run += s[i];
-      }
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kl = (i >> 2) * 8 + half * 4 + (i & 3);
-          const float a = v_lds[buf][kl * C::VROW + dt * 32 + l32];
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, s[i], o[dt], 0, 0, 0);
+          for (int i = 1; i < 16; ++i) r = fmaxf(r, s[i]);
+          mx = r * sl2;
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const bool grow = mx > m_run + kSlack;
+        if (__ballot(grow)) {
+          const float m_new = grow ? mx : m_run;
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+          m_run = m_new;
+          l_run *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+        }
+        const float base = m_run == -INFINITY ? 0.f : m_run;
+        if (scaled) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            s[i] = __builtin_amdgcn_exp2f(s[i] - base);
+            l_run += s[i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            s[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -base));
+            l_run += s[i];
+          }
+        }
+        __builtin_amdgcn_s_setprio(3);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kl = (i >> 2) * 8 + half * 4 + (i & 3);
+            const float a = vt[kl * C::VROW + dt * 32 + l32];
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, s[i], o[dt], 0, 0, 0);
+          }
+        __builtin_amdgcn_s_setprio(0);
+      }
     }
-    if (t + 1 < ntiles) lstore(buf ^ 1);
+    if (st + 1 < nstages) lstore(buf ^ 1);
     __syncthreads();
   }
 
@@ -231,21 +301,6 @@ __global__ __launch_bounds__(kNT, (D == 128 && MASK) ? 1 : 2) void flash_f32_ker
 // every per-lane offset is fixed for the whole kernel (the tile moves the
 // resource base, a scalar operation).
 constexpr int kSW = 4;  // wavefronts (key splits) per workgroup
-
-// Bytes from the first to the last valid element of `rows` rows of D floats
-// at `stride` floats apart (0 when no row is valid).
-template <int D>
-__device__ __forceinline__ int rows_extent(int rows, int64_t stride) {
-  return rows > 0 ? (int)(((int64_t)(rows - 1) * stride + D) * 4) : 0;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const float* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, bytes, 0x00020000);
-}
-
-__device__ __forceinline__ f32x4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 // NDT consecutive floats (NDT = 2 or 4).
 template <int NDT>
@@ -495,6 +550,10 @@ bool flash_f32_supports(const SdpaParams& p) {
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 4 || p.ks[i] % 4 || p.vs[i] % 4 || p.os[i] % 4) return false;
+  // K/V stages (up to 64 rows) are read through buffer resources with
+  // 32-bit lane offsets.
+  for (int64_t st : {p.ks[2], p.vs[2]})
+    if (st < 0 || st >= (int64_t(1) << 23)) return false;
   return true;
 }
 
