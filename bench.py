@@ -42,10 +42,33 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+# Untimed run time before a workload's warm-up calls.  The GPU's clocks rise
+# only under sustained load: measured on config 3, the first ~50 ms of
+# back-to-back launches run up to 20% slower than the steady state that a
+# training or serving loop sees, so a handful of warm-up calls alone would
+# time the ramp, not the kernel.
+PREWARM_S = 0.25
+
+
+def prewarm(torch, fn, seconds: float = PREWARM_S) -> int:
+    """Calls fn() untimed, in batches of 10, until `seconds` of wall time
+    have passed; returns the number of calls."""
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        n += 10
+        if time.perf_counter() - t0 >= seconds:
+            return n
+
+
 def time_launches(torch, fn, steps: int, warmup: int):
-    """Average ms per call of fn() over `steps` calls after `warmup` calls,
-    timed with events on the current stream; also returns the median of the
-    per-call event durations."""
+    """Average ms per call of fn() over `steps` calls after a PREWARM_S
+    pre-warm and `warmup` calls, timed with events on the current stream;
+    also returns the median of the per-call event durations."""
+    prewarm(torch, fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -505,6 +528,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm_s": PREWARM_S,
         "ms_per_step": round(c3["avg_ms"], 6),
         "higher_is_better": True,
         "scaling": "weak",

@@ -10,21 +10,26 @@
 // v_mfma_f32_32x32x16_bf16, P taken from the S^T accumulator, V^T fragments
 // from transposing LDS reads.
 //
-// The difference is the schedule.  Each wavefront keeps two S tiles in
-// registers and runs, per tile t,
-//   phase A: S(t+1) = K(t+1) Q^T, one MFMA at a time, with the exp2 / bf16 /
-//            row-sum work of S(t) placed between the MFMAs, and
-//   phase B: O^T += V^T(t) P(t)^T, with the row max of S(t+1) placed between
-//            the MFMAs,
-// so the vector work of the softmax runs in the matrix core's shadow instead
-// of between its bursts.  The LDS operand reads are inline asm issued a fixed
-// distance ahead of their MFMAs, each followed by an lgkmcnt wait that counts
-// the reads issued after it (LDS reads complete in order); the compiler
-// therefore adds no waits of its own for the LDS-DMA into the other stage.
-// sched_barrier fences keep this interleave as written.
+// The difference is the schedule and the softmax's vector work.  There is
+// no per-tile row max: a row's exp2 base is its first tile's max, and a tile
+// whose row sum passes kSumCap (a score more than 11 above the base, in log2
+// units) takes a rare path that raises the base, rescales O and l, and
+// recomputes that tile's P.  Per tile and wavefront the vector work is 32
+// FMA + exp2, 16 bf16 packs and 16 dot2 row sums, spread evenly over the 32
+// MFMAs (the exp2 is the one costly instruction: about 2.5 ns per MFMA it
+// shares a slot with, where FMAs and packs are free):
+//   phase A: S(t+1) = K(t+1) Q^T, with the exp2 of keys 32-63 of S(t)
+//            between the MFMAs;
+//   phase B: O^T += V^T(t) P(t)^T, with the exp2 of keys 0-31 of S(t+1)
+//            between the MFMAs.
+// The LDS operand reads are inline asm issued a fixed distance ahead of their
+// MFMAs, each followed by an lgkmcnt wait that counts the reads issued after
+// it (LDS reads complete in order); the compiler therefore adds no waits of
+// its own for the LDS-DMA into the other stage.  sched_barrier fences keep
+// this interleave as written.
 //
-// A wavefront's last tile also computes S of the K stage behind it; that S
-// is never used (its max is replaced by -inf), which keeps one code path in
+// A wavefront's last tile also computes S of the K stage behind it (and the
+// exp2 of half of it); that S is never used, which keeps one code path in
 // the loop and the register allocation spill-free.
 #include <type_traits>
 
@@ -42,6 +47,9 @@ constexpr int kPfV = 4;   // V read pairs issued ahead of their PV MFMA
 constexpr int kHeadGroup = 4;  // heads whose q-blocks an XCD issues together
 
 using tiles::kSlack;
+// Row-sum cap of one tile (32 keys per lane): a sum above it (or NaN) means a
+// score passed the base by more than log2(kSumCap / 32) = 11 > kSlack.
+constexpr float kSumCap = 65536.f;
 using tiles::s16x4;
 using tiles::tile_swz;
 using tiles::wait_dma;
@@ -65,12 +73,6 @@ __device__ __forceinline__ void lgkm_tie(s16x4& a, s16x4& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
-// m = max(m, x, y) without the NaN-quieting copies the compiler adds to fmaxf.
-// Only used far (many MFMAs) after the MFMAs that wrote x and y: the compiler
-// does not add the MFMA -> VALU wait states for inline asm.
-__device__ __forceinline__ void max3(float& m, float x, float y) {
-  asm("v_max3_f32 %0, %0, %1, %2" : "+v"(m) : "v"(x), "v"(y));
-}
 
 // f(integral_constant<int, J>) for J = B .. E-1, in order.
 template <int B, int E, class F>
@@ -83,10 +85,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // K / V tile loader: rows [t*kBN, t*kBN + kBN) of one (batch, head) into a
 // swizzled LDS tile.  Instruction i of a wavefront covers rows
-// i*STEP + wave*RPI + lane/DCH of the tile.  Its buffer resource, built once,
-// starts at row i*STEP and ends at the tensor's last row; the tile offset
-// goes into the per-lane offset, which the hardware range-checks, so rows
-// past Tk read as zeros and no address leaves the tensor.
+// i*STEP + wave*RPI + lane/DCH of the tile.  One buffer resource spans the
+// tensor's Tk rows; the tile, instruction and lane offsets all go into the
+// per-lane offset, which the hardware range-checks, so rows past Tk read as
+// zeros and no address leaves the tensor.
 template <int D>
 struct Loader {
   static constexpr int DCH = D / 8;
@@ -95,23 +97,19 @@ struct Loader {
   static constexpr int STEP = kNW * RPI;
   static_assert(STEP % tiles::kSwzPeriod<D> == 0 && kBN % tiles::kSwzPeriod<D> == 0, "one offset per lane");
 #if defined(__HIP_DEVICE_COMPILE__)
-  __amdgpu_buffer_rsrc_t rsrc[LOADS];
+  __amdgpu_buffer_rsrc_t rsrc;
 #endif
   uint32_t voff;
   uint32_t tile_bytes;
+  uint32_t step_bytes;
   __device__ __forceinline__ Loader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
     tile_bytes = (uint32_t)(kBN * row_stride * 2);
+    step_bytes = (uint32_t)(STEP * row_stride * 2);
     const int row = wave * RPI + lane / DCH, slot = lane % DCH;
     voff = (uint32_t)(((int64_t)row * row_stride + (slot ^ tile_swz<D>(row)) * 8) * 2);
 #if defined(__HIP_DEVICE_COMPILE__)
-    const int64_t nbytes = (int64_t)Tk * row_stride * 2;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int64_t off = (int64_t)i * STEP * row_stride * 2;
-      const int64_t rem = nbytes - off;
-      rsrc[i] = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(const_cast<bf16*>(b)) + off, (short)0,
-                                                  rem > 0 ? (int)rem : 0, 0x00020000);
-    }
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(b), (short)0, (int)((int64_t)Tk * row_stride * 2),
+                                             0x00020000);
 #endif
   }
   __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
@@ -119,8 +117,8 @@ struct Loader {
     const uint32_t vo = voff + (uint32_t)t * tile_bytes;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[i], (tiles::lds_void_t*)(lds + (kNW * i + wave) * 64 * 8), 16, vo,
-                                               0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (tiles::lds_void_t*)(lds + (kNW * i + wave) * 64 * 8), 16,
+                                               vo + (uint32_t)i * step_bytes, 0, 0, 0);
 #endif
   }
 };
@@ -137,10 +135,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   constexpr int TB = TILE * 2;      // its bytes
   constexpr int MS = 2 * (D / 16);  // S MFMAs per tile
   constexpr int MP = 4 * (D / 32);  // PV MFMAs per tile
-  constexpr int GP = 16 / MS;       // exp pairs per S MFMA
-  constexpr int MH = MP / 2;        // PV MFMAs that carry the max work
-  constexpr int XP = 16 / MH;       // max3 ops per such MFMA
-  static_assert(16 % MS == 0 && 16 % MH == 0, "interleave");
+  static_assert(MS % 8 == 0 || 8 % MS == 0, "interleave");
   __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 K1 V0 V1
 
   const int tid = threadIdx.x;
@@ -241,13 +236,14 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-  // Running exp2 base (log2 units, shared by lanes l and l^32), the lane's
-  // partial row sum, and -base for the exp FMA.
-  float b_run = -INFINITY, l_run = 0.f;
-  float nbase = 0.f;
+  // Running exp2 base of the row (log2 units, shared by lanes l and l^32),
+  // -base for the exp2 FMA, and the lane's partial row sum.
+  float b_run = 0.f, nbase = 0.f, l_run = 0.f;
   const float sl2 = p.scale_log2;  // > 0 (checked on the host)
-  f32x16 s0[2], s1[2];  // S^T of two tiles: 2 x 32 keys, lane = query
-  u32x4 pb[4];          // P of the current tile: 4 x 16 keys, bf16 pairs
+  f32x16 s0[2], s1[2];   // S^T of two tiles: 2 x 32 keys, lane = query
+  u32x4 pf0[2], pf1[2];  // P of keys 0-31 (16-key steps 0, 1) of even / odd tiles, bf16 pairs
+  u32x4 pb[2];           // P of keys 32-63 (steps 2, 3) of the current tile
+  float lf = 0.f;        // row-sum part of keys 0-31 of the next tile
 
   // Masks S of tile t per element where keys pass Tk or the diagonal.
   auto mask_tile = [&](f32x16 (&s)[2], int t) {
@@ -260,48 +256,55 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
         if (key >= Tk || (CAUSAL && key > qi)) s[mt][i] = -INFINITY;
       }
   };
-  // Row max of S (16 in-lane values + lane l^32) -> lazy base update: the
-  // base only moves when the max passes it by kSlack, and O and l move with it.
-  auto finish_max = [&](float mx) {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    const float m_l2 = mx * sl2;
-    const bool need = m_l2 > b_run + kSlack;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      const float nb = need ? m_l2 : b_run;
-      const float alpha = need ? __builtin_amdgcn_exp2f(b_run - nb) : 1.f;
-      b_run = nb;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-    }
-    nbase = b_run == -INFINITY ? 0.f : -b_run;
-  };
-  auto full_max = [&](f32x16 (&s)[2]) -> float {
+  // Row max of S: 32 in-lane values, then lanes l and l^32.
+  auto row_max = [&](f32x16 (&s)[2]) -> float {
     float m0 = -INFINITY, m1 = -INFINITY;
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
       const float x = s[g >> 3][(g & 7) * 2], y = s[g >> 3][(g & 7) * 2 + 1];
-      // fmaxf: used right after MFMAs, where the compiler's wait states count.
       if (g & 1) m1 = fmaxf(m1, fmaxf(x, y));
       else m0 = fmaxf(m0, fmaxf(x, y));
     }
-    return fmaxf(m0, m1);
+    const float mx = fmaxf(m0, m1);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   };
-  // exp2 of pair g of S into P (bf16) and the row sum of exactly those bf16
-  // values (two per dot2).
+  // exp2 of pair g of S (keys 2g, 2g+1 of the lane's 32) into P (bf16) and
+  // the row sum of exactly those bf16 values.
   const bf16x2 one2 = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
-  float lsum0 = 0.f, lsum1 = 0.f;
-  auto exp_pair = [&](f32x16 (&s)[2], int g) {
+  auto exp_pair = [&](f32x16 (&s)[2], int g, u32x4 (&dst)[2], float& acc) {
     const int mt = g >> 3, i = (g & 7) * 2;
     const float p0 = __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
     const float p1 = __builtin_amdgcn_exp2f(fmaf(s[mt][i + 1], sl2, nbase));
     const bf16x2 w = {static_cast<bf16>(p0), static_cast<bf16>(p1)};
-    pb[mt * 2 + (i >> 3)][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, w);
-    if (g & 1) lsum1 = __builtin_amdgcn_fdot2_f32_bf16(w, one2, lsum1, false);
-    else lsum0 = __builtin_amdgcn_fdot2_f32_bf16(w, one2, lsum0, false);
+    const uint32_t wu = __builtin_bit_cast(uint32_t, w);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(w, one2, acc, false);
+    // Keeps the work in this MFMA's slot: without a use here the compiler
+    // sinks it past the branches between the phases, behind the MFMAs.
+    asm volatile("" ::"v"(wu), "v"(acc));
+    dst[i >> 3][(i & 7) >> 1] = wu;
+  };
+  // A tile whose row sum passed kSumCap has a score above the base by more
+  // than log2(kSumCap / 32) > kSlack: raise the base of such rows to their
+  // max, rescale O and l to it, and recompute the tile's P.  Returns the
+  // tile's new row sum.
+  auto rebase = [&](f32x16 (&sc)[2], u32x4 (&pc)[2]) -> float {
+    const float rel = row_max(sc) * sl2 - b_run;
+    const float d = rel > kSlack ? rel : 0.f;
+    const float alpha = __builtin_amdgcn_exp2f(-d);
+    b_run += d;
+    nbase = -b_run;
+    l_run *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) exp_pair(sc, g, pc, a0);
+#pragma unroll
+    for (int g = 8; g < 16; ++g) exp_pair(sc, g, pb, a1);
+    return a0 + a1;
   };
 
   // S of the tile in K stage 0, not interleaved (before the loop).
@@ -322,9 +325,13 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     for (int j = 0; j < MS; ++j) s[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], s[j & 1], 0, 0, 0);
   };
 
-  // One tile (phases A and B above); returns the row max of S_next before
-  // masking.  K stage KS holds tile t+1, V stage VS tile t.
-  auto tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], auto ks_tag, auto vs_tag) -> float {
+  // One tile t: K stage KS holds tile t+1, V stage VS tile t; sc = S(t)
+  // (keys 0-31 already exponentiated into pc), sn receives S(t+1).
+  //   phase A: the S(t+1) MFMAs, with the exp2 of keys 32-63 of S(t) between them;
+  //   phase B: the PV(t) MFMAs, with the exp2 of keys 0-31 of S(t+1) (into pn) between them.
+  // The row-sum check between the phases runs the rebase before P(t) is used.
+  auto tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pc)[2], u32x4 (&pn)[2], int t, auto ks_tag,
+                  auto vs_tag) {
     constexpr int KS = decltype(ks_tag)::value;
     constexpr int VB = (2 + decltype(vs_tag)::value) * TB;
     bf16x8 kr[MS];
@@ -340,8 +347,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       ds_tr<VB + ks * 16 * D * 2>(vr[j][0], va[dt][0]);
       ds_tr<VB + ks * 16 * D * 2>(vr[j][1], va[dt][1]);
     };
-    lsum0 = 0.f;
-    lsum1 = 0.f;
+    float ls = 0.f;
     static_for<0, kPfK>(rdk);
     fence();
     static_for<0, MS>([&](auto j_tag) {
@@ -353,13 +359,16 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       else
         sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], sn[j & 1], 0, 0, 0);
 #pragma unroll
-      for (int g = j * GP; g < (j + 1) * GP; ++g) exp_pair(sc, g);
+      for (int g = 8 + j * 8 / MS; g < 8 + (j + 1) * 8 / MS; ++g) exp_pair(sc, g, pb, ls);
       fence();
     });
-    l_run += lsum0 + lsum1;
+    if (t + 1 < nw && edge(t + 1)) mask_tile(sn, t + 1);
+    float lt = lf + ls;
+    if (__builtin_amdgcn_ballot_w64(!(lt <= kSumCap))) lt = rebase(sc, pc);
+    l_run += lt;
+    lf = 0.f;
     static_for<0, kPfV>(rdv);
     fence();
-    float m0 = -INFINITY, m1 = -INFINITY;
     static_for<0, MP>([&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
       constexpr int dt = j % (D / 32), ks = j / (D / 32);
@@ -367,18 +376,12 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       lgkm_tie<wait_v(j, MP)>(vr[j][0], vr[j][1]);
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pb[ks]), o[dt], 0, 0, 0);
-      if constexpr (j >= MP - MH) {
+      const u32x4 pbk = ks < 2 ? pc[ks & 1] : pb[ks & 1];
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pbk), o[dt], 0, 0, 0);
 #pragma unroll
-        for (int g = (j - (MP - MH)) * XP; g < (j - (MP - MH) + 1) * XP; ++g) {
-          const float x = sn[g >> 3][(g & 7) * 2], y = sn[g >> 3][(g & 7) * 2 + 1];
-          if (g & 1) max3(m1, x, y);
-          else max3(m0, x, y);
-        }
-      }
+      for (int g = j * 8 / MP; g < (j + 1) * 8 / MP; ++g) exp_pair(sn, g, pn, lf);
       fence();
     });
-    return fmaxf(m0, m1);
   };
 
   wait_dma();
@@ -386,30 +389,27 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   if (nw > 0) {
     s_plain(s0);
     if (edge(0)) mask_tile(s0, 0);
-    finish_max(full_max(s0));
+    const float mx = row_max(s0);
+    b_run = mx == -INFINITY ? 0.f : mx * sl2;
+    nbase = -b_run;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) exp_pair(s0, g, pf0, lf);
   }
   // Iteration t: K(t+1) in K stage (t+1)&1, V(t) in V stage t&1; loads K(t+2)
   // into K stage t&1 and V(t+1) into V stage (t+1)&1, whose previous tiles
   // every wavefront has finished reading at the barrier.
-  auto iter = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], auto par_tag) {
+  auto iter = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pc)[2], u32x4 (&pn)[2], auto par_tag) {
     constexpr int PAR = decltype(par_tag)::value;  // t & 1
     wait_dma();
     __syncthreads();
     if (t + 2 < N) kload.load(t + 2, kst[PAR], wave);
     if (t + 1 < N) vload.load(t + 1, vst[PAR ^ 1], wave);
-    if (t < nw) {
-      float mx = tile(sc, sn, std::integral_constant<int, PAR ^ 1>{}, std::integral_constant<int, PAR>{});
-      if (t + 1 < nw && edge(t + 1)) {
-        mask_tile(sn, t + 1);
-        mx = full_max(sn);
-      }
-      finish_max(t + 1 < nw ? mx : -INFINITY);
-    }
+    if (t < nw) tile(sc, sn, pc, pn, t, std::integral_constant<int, PAR ^ 1>{}, std::integral_constant<int, PAR>{});
   };
   for (int t = 0; t < N; t += 2) {
-    iter(t, s0, s1, std::integral_constant<int, 0>{});
+    iter(t, s0, s1, pf0, pf1, std::integral_constant<int, 0>{});
     if (t + 1 >= N) break;
-    iter(t + 1, s1, s0, std::integral_constant<int, 1>{});
+    iter(t + 1, s1, s0, pf1, pf0, std::integral_constant<int, 1>{});
   }
 
   const float lt = l_run + __shfl_xor(l_run, 32, 64);

@@ -297,6 +297,38 @@ def test_sdpa_btnh_layout_gqa_and_mask(cuda, nat, oracle, dtype):
     check_sdpa(out, ref, dtype)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("case", ["growing", "spike", "shrinking", "wide_scale"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_flash_bf16_rebase(cuda, nat, oracle, D, case, causal):
+    """Score ranges that move the mask-free bf16 kernel's exp2 base after the
+    first tile: keys whose scale grows along the sequence (later tiles pass
+    the first tile's max by far more than the slack), one key with a huge
+    score in a late tile, keys that shrink after the first tile (the base
+    stays high and later probabilities are small), and a scale four times
+    1/sqrt(D).  Every row against the fp64 oracle on the same bf16 inputs."""
+    B, H, T = 1, 4, 1000
+    rng = np.random.default_rng(31)
+    q = rng.standard_normal((B, H, T, D))
+    k = rng.standard_normal((B, H, T, D))
+    v = rng.standard_normal((B, H, T, D))
+    scale = D ** -0.5
+    j = np.arange(T)[None, None, :, None]
+    if case == "growing":
+        k = k * (1 + 4 * j / T)
+    elif case == "spike":
+        k[:, :, 700] *= 30
+    elif case == "shrinking":
+        k = k * (5 / (1 + 4 * j / T))
+    else:
+        scale = 4 * D ** -0.5
+    qd, kd, vd = (dev(cuda, a, cuda.bfloat16) for a in (q, k, v))
+    assert nat.sdpa_kernel_name(qd, kd, vd, causal=causal) == f"flash_bf16_d{D}"
+    out = nat.sdpa(qd, kd, vd, scale=scale, causal=causal)
+    ref = oracle.sdpa(host(qd), host(kd), host(vd), scale, causal=causal)
+    check_sdpa(out, ref, "bf16")
+
+
 def test_sdpa_bf16_golden(cuda, nat, golden):
     q, k, v = (dev(cuda, golden[f"sdpa_bf16_{s}"], cuda.bfloat16) for s in "qkv")
     out = nat.sdpa(q, k, v, scale=float(golden["sdpa_bf16_scale"]), causal=True)
