@@ -43,6 +43,11 @@ using tiles::lds_s16x4_t;
 using tiles::s16x4;
 using tiles::tile_swz;
 using tiles::wait_dma;
+using tiles::ds_b128;
+using tiles::ds_tr;
+using tiles::lgkm_tie;
+using tiles::fence;
+using tiles::static_for;
 template <int D>
 using Loader = tiles::TileLoader<D, kTile, kNT / 64>;
 
@@ -268,12 +273,17 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
 
 // ----------------------------------------------------------------------- dQ
 
+// Operand reads issued ahead of their MFMAs in the dQ kernel (K / V row
+// fragment pairs, transposed K fragment pairs).
+constexpr int kDqPf = 2;
+
 template <int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdParams p) {
-  __shared__ __attribute__((aligned(16))) bf16 k0[kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 v0[kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 k1[kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 v1[kTile * D];
+__global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
+  constexpr int TILE = kTile * D;  // elements of one K or V tile
+  constexpr int TB = TILE * 2;     // its bytes
+  constexpr int NK = D / 16;       // S (and dP) MFMAs per 32-key block
+  constexpr int NT = 2 * (D / 32);  // dQ MFMAs per 32-key block
+  __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 V0 K1 V1
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -305,11 +315,11 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
   if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kRows));
   const int ntiles = (kv_end + kTile - 1) / kTile;
   const Loader<D> kload(kp, p.ks[2], Tk, wave, lane), vload(vp, p.vs[2], Tk, wave, lane);
-  auto issue = [&](int t, bf16* kl, bf16* vl) {
-    kload.load(t, kl, wave);
-    vload.load(t, vl, wave);
+  auto issue = [&](int t, int st) {
+    kload.load(t, smem + (2 * st) * TILE, wave);
+    vload.load(t, smem + (2 * st + 1) * TILE, wave);
   };
-  if (ntiles > 0) issue(0, k0, v0);
+  if (ntiles > 0) issue(0, 0);
 
   bf16x8 qf[D / 16], gf[D / 16];
   load_frags<D>(static_cast<const bf16*>(p.q) + b * p.qs[0] + h * p.qs[1], p.qs[2], qi, Tq, half, qf);
@@ -341,24 +351,67 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
     for (int i = 0; i < 16; ++i) dq[dt][i] = 0.f;
 
   const float sl2 = p.scale_log2;
-  const int rsw = tile_swz<D>(l32);
-  const TrReader<D> tr(lane);
+  // LDS byte addresses of the operand reads; the stage, the 32-key block and
+  // the 16-key step are immediate offsets.
+  const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem;
+  uint32_t ra[D / 16];  // row l32 of a 32-key block, feature chunk kk
+  {
+    const int rsw = tile_swz<D>(l32);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) ra[kk] = base + (uint32_t)((l32 * D + ((kk * 2 + half) ^ rsw) * 8) * 2);
+  }
+  uint32_t ta[D / 32][2];  // transposing reads of K (the order of TrReader)
+  {
+    const int tj = lane & 15, tg = (lane >> 4) & 1;
+    const int r = 4 * half + (tj >> 2);
+    const int sw = tile_swz<D>(r), sw8 = tile_swz<D>(r + 8);
+    const int chunk = tg * 2 + ((tj & 3) >> 1), sub = (tj & 1) * 4;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      ta[dt][0] = base + (uint32_t)((r * D + sub + ((dt * 4 + chunk) ^ sw) * 8) * 2);
+      ta[dt][1] = base + (uint32_t)(((r + 8) * D + sub + ((dt * 4 + chunk) ^ sw8) * 8) * 2);
+    }
+  }
 
-  auto block = [&](const bf16* kl, const bf16* vl, int kb, int mt, auto edge_tag) __attribute__((always_inline)) {
+  // One 32-key block (MT) of the tile in stage ST:
+  //   S^T = K Q^T and dP^T = V dO^T, their MFMAs alternating, K and V row
+  //   fragments read kDqPf pairs ahead; dS = P (dP - delta); then
+  //   dQ^T += K^T dS^T with the transposed K fragments read kDqPf ahead.
+  auto block = [&](auto st_tag, auto mt_tag, int kb, auto edge_tag) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st_tag)::value, MT = decltype(mt_tag)::value;
     constexpr bool EDGE = decltype(edge_tag)::value;
+    constexpr int KO = 2 * ST * TB + MT * 32 * D * 2;  // K rows of this block
+    constexpr int VO = KO + TB;                        // V rows
+    constexpr int KT = 2 * ST * TB;                    // K tile (transposing reads)
+    bf16x8 kf[NK], vf[NK];
+    auto rd = [&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      ds_b128<KO>(kf[j], ra[j]);
+      ds_b128<VO>(vf[j], ra[j]);
+    };
     f32x16 s, dp;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(kl, mt, kk, l32, half, rsw), qf[kk], s, 0, 0, 0);
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(vl, mt, kk, l32, half, rsw), gf[kk], dp, 0, 0, 0);
+    static_for<0, kDqPf>(rd);
+    fence();
+    static_for<0, NK>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      if constexpr (j + kDqPf < NK) rd(std::integral_constant<int, j + kDqPf>{});
+      constexpr int ahead = 2 * (kDqPf < NK - 1 - j ? kDqPf : NK - 1 - j);
+      lgkm_tie<ahead + 1>(kf[j]);
+      if constexpr (j == 0)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], f32x16{}, 0, 0, 0);
+      else
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], s, 0, 0, 0);
+      lgkm_tie<ahead>(vf[j]);
+      if constexpr (j == 0)
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j], gf[j], f32x16{}, 0, 0, 0);
+      else
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j], gf[j], dp, 0, 0, 0);
+      fence();
+    });
     bf16x8 db[2];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = kb + mt * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+      const int key = kb + MT * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
       float x = s[i] * sl2;
       if constexpr (MASK) {
         if (qi < Tq && key < Tk)
@@ -372,38 +425,53 @@ __global__ __launch_bounds__(kNT, D == 128 ? 1 : 2) void bwd_dq_mfma(SdpaBwdPara
       }
       db[i >> 3][i & 7] = static_cast<bf16>(pr * (dp[i] - dl));
     }
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr.read(kl, mt * 2 + ks, dt), db[ks], dq[dt], 0, 0, 0);
+    // dQ MFMA j: d-block j % (D/32), 16-key step j / (D/32) of this block.
+    s16x4 tr[NT][2];
+    auto rdt = [&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      ds_tr<KT + (MT * 2 + ks) * 16 * D * 2>(tr[j][0], ta[dt][0]);
+      ds_tr<KT + (MT * 2 + ks) * 16 * D * 2>(tr[j][1], ta[dt][1]);
+    };
+    static_for<0, kDqPf>(rdt);
+    fence();
+    static_for<0, NT>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      if constexpr (j + kDqPf < NT) rdt(std::integral_constant<int, j + kDqPf>{});
+      lgkm_tie<2 * (kDqPf < NT - 1 - j ? kDqPf : NT - 1 - j)>(tr[j][0], tr[j][1]);
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(tr[j][0], tr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
+      dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db[ks], dq[dt], 0, 0, 0);
+      fence();
+    });
   };
 
-  auto step = [&](int t, const bf16* kl, const bf16* vl) __attribute__((always_inline)) {
+  auto step = [&](int t, auto st_tag) __attribute__((always_inline)) {
     const int kb = t * kTile;
     if (q0 >= Tq) return;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int k0r = kb + mt * 32;
-      if (k0r >= Tk || (CAUSAL && k0r > q0 + 31)) continue;  // nothing of this block is visible
+    static_for<0, 2>([&](auto mt_tag) {
+      constexpr int MT = decltype(mt_tag)::value;
+      const int k0r = kb + MT * 32;
+      if (k0r >= Tk || (CAUSAL && k0r > q0 + 31)) return;  // nothing of this block is visible
       const bool edge = (k0r + 32 > Tk) || (CAUSAL && k0r + 31 > q0);
       if (edge)
-        block(kl, vl, kb, mt, std::true_type{});
+        block(st_tag, mt_tag, kb, std::true_type{});
       else
-        block(kl, vl, kb, mt, std::false_type{});
-    }
+        block(st_tag, mt_tag, kb, std::false_type{});
+    });
   };
 
   wait_dma();
   __syncthreads();
   for (int t = 0; t < ntiles; t += 2) {
-    if (t + 1 < ntiles) issue(t + 1, k1, v1);
-    step(t, k0, v0);
+    if (t + 1 < ntiles) issue(t + 1, 1);
+    step(t, std::integral_constant<int, 0>{});
     wait_dma();
     __syncthreads();
     if (t + 1 >= ntiles) break;
-    if (t + 2 < ntiles) issue(t + 2, k0, v0);
-    step(t + 1, k1, v1);
+    if (t + 2 < ntiles) issue(t + 2, 0);
+    step(t + 1, std::integral_constant<int, 1>{});
     wait_dma();
     __syncthreads();
   }

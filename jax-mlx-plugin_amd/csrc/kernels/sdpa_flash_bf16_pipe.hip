@@ -53,35 +53,11 @@ constexpr float kSumCap = 65536.f;
 using tiles::s16x4;
 using tiles::tile_swz;
 using tiles::wait_dma;
-
-template <int IMM>
-__device__ __forceinline__ void ds_b128(bf16x8& r, uint32_t a) {
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(IMM));
-}
-template <int IMM>
-__device__ __forceinline__ void ds_tr(s16x4& r, uint32_t a) {
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(IMM));
-}
-// s_waitcnt lgkmcnt(N) that the named registers depend on, so their uses are
-// not scheduled (or copied) before it.
-template <int N>
-__device__ __forceinline__ void lgkm_tie(bf16x8& r) {
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
-}
-template <int N>
-__device__ __forceinline__ void lgkm_tie(s16x4& a, s16x4& b) {
-  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
-}
-__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// f(integral_constant<int, J>) for J = B .. E-1, in order.
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
+using tiles::ds_b128;
+using tiles::ds_tr;
+using tiles::lgkm_tie;
+using tiles::fence;
+using tiles::static_for;
 
 // K / V tile loader: rows [t*kBN, t*kBN + kBN) of one (batch, head) into a
 // swizzled LDS tile.  Instruction i of a wavefront covers rows

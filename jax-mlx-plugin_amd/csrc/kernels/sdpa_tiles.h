@@ -2,6 +2,8 @@
 // split-KV decode): swizzled K/V tiles filled by asynchronous LDS-DMA loads.
 #pragma once
 
+#include <type_traits>
+
 #include "sdpa_common.h"
 
 namespace mfx {
@@ -32,6 +34,39 @@ __host__ __device__ constexpr int tile_swz(int r) {
 }
 template <int D>
 constexpr int kSwzPeriod = D == 128 ? 16 : 8;
+
+// LDS operand reads as inline asm at an immediate byte offset from a
+// per-lane LDS address, so the compiler neither batches them nor adds waits
+// of its own; callers wait with lgkm_tie.
+template <int IMM>
+__device__ __forceinline__ void ds_b128(bf16x8& r, uint32_t a) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(IMM));
+}
+template <int IMM>
+__device__ __forceinline__ void ds_tr(s16x4& r, uint32_t a) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(IMM));
+}
+// s_waitcnt lgkmcnt(N) that the named registers depend on, so their uses are
+// not scheduled (or copied) before it.  LDS reads complete in order, so N is
+// the number of reads issued after the one the registers came from.
+template <int N>
+__device__ __forceinline__ void lgkm_tie(bf16x8& r) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_tie(s16x4& a, s16x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// f(integral_constant<int, J>) for J = B .. E-1, in order.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // s_waitcnt vmcnt(0), other counters left alone: this wave's LDS-DMA
 // loads have landed.
