@@ -111,14 +111,30 @@ __device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int hal
 
 // ----------------------------------------------------------------- dK, dV
 
+// dK / dV run one wavefront per SIMD at d = 128 (the 32 keys' K and V
+// operands and dK / dV accumulators alone take 192 registers), so the
+// kernel overlaps its own vector and matrix work: per 32-query block i,
+//   X(i):        S(i) and dP(i) MFMAs (Q / dO row fragments streamed ahead);
+//   Y(i-1) | V(i): the dV and dK MFMAs of block i-1, with the exp2 / dS
+//                work of block i (V) placed between them.
+// Y(i-1) reads block i-1's Q / dO tile, which may be the previous tile, so
+// tiles cycle through three LDS stages (one workgroup per CU has the LDS).
+// Every block runs, also those a causal mask hides from this wavefront's
+// keys: their P and dS are masked to zero, no branch breaks the pipeline,
+// and the wavefront with the most visible blocks sets the pace anyway.
+constexpr int kKvPf = 2;   // operand reads issued ahead of their MFMAs
+constexpr int kKvStages = 3;
+
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
-  __shared__ __attribute__((aligned(16))) bf16 q0[kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 g0[kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 q1[kTile * D];
-  __shared__ __attribute__((aligned(16))) bf16 g1[kTile * D];
-  __shared__ __attribute__((aligned(16))) float st0[2 * kTile];  // lse | delta
-  __shared__ __attribute__((aligned(16))) float st1[2 * kTile];
+  constexpr int TILE = kTile * D;    // elements of one Q or dO tile
+  constexpr int TB = TILE * 2;       // its bytes
+  constexpr int NK = D / 16;         // S (and dP) MFMAs per block
+  constexpr int NT = 2 * (D / 32);   // dV (and dK) MFMAs per block
+  constexpr int GB = kKvStages * TB;           // byte offset of the dO stages
+  constexpr int LB = 2 * kKvStages * TB;       // byte offset of the lse / delta rows
+  constexpr int LS = 2 * kTile * 4;            // their bytes per stage (lse | delta)
+  __shared__ __attribute__((aligned(16))) char smem[LB + kKvStages * LS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -160,15 +176,18 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   gload.nbytes = (int)(((int64_t)(G - 1) * p.dos[1] + (int64_t)(Tq - 1) * p.dos[2] + D) * 2);
   auto tile_head = [&](int t) { return t / per_head; };
   auto tile_q = [&](int t) { return qt0 + t % per_head; };
-  auto issue = [&](int t, bf16* ql, bf16* gl, float* sl) {
+  auto issue = [&](int t, int st) {
     const int g = tile_head(t), qt = tile_q(t);
-    qload.load_at((uint32_t)(((int64_t)g * p.qs[1] + (int64_t)qt * kTile * p.qs[2]) * 2), ql, wave);
-    gload.load_at((uint32_t)(((int64_t)g * p.dos[1] + (int64_t)qt * kTile * p.dos[2]) * 2), gl, wave);
+    qload.load_at((uint32_t)(((int64_t)g * p.qs[1] + (int64_t)qt * kTile * p.qs[2]) * 2),
+                  reinterpret_cast<bf16*>(smem + st * TB), wave);
+    gload.load_at((uint32_t)(((int64_t)g * p.dos[1] + (int64_t)qt * kTile * p.dos[2]) * 2),
+                  reinterpret_cast<bf16*>(smem + GB + st * TB), wave);
     const uint32_t soff = (uint32_t)(((int64_t)g * Tq + (int64_t)qt * kTile) * 4);
+    float* sl = reinterpret_cast<float*>(smem + LB + st * LS);
     if (wave == 0) tiles::load_row64_f32(lsep, st_bytes, soff, sl, lane);
     if (wave == 1) tiles::load_row64_f32(dlp, st_bytes, soff, sl + kTile, lane);
   };
-  if (ntiles > 0) issue(0, q0, g0, st0);
+  if (ntiles > 0) issue(0, 0);
 
   bf16x8 kf[D / 16], vf[D / 16];
   load_frags<D>(kp, p.ks[2], key, Tk, half, kf);
@@ -181,86 +200,205 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
     for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
 
   const float sl2 = p.scale_log2;
-  const int rsw = tile_swz<D>(l32);
-  const TrReader<D> tr(lane);
+  // LDS byte addresses of the operand reads (stage, 32-query block and
+  // 16-query step are immediate offsets).
+  const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem;
+  uint32_t ra[D / 16], rg[D / 16];  // row l32 of a 32-query block, feature chunk kk (Q | dO)
+  {
+    const int rsw = tile_swz<D>(l32);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      ra[kk] = base + (uint32_t)((l32 * D + ((kk * 2 + half) ^ rsw) * 8) * 2);
+      rg[kk] = ra[kk] + GB;
+    }
+  }
+  uint32_t ta[D / 32][2], tg[D / 32][2];  // transposing reads (the order of TrReader), Q | dO
+  {
+    const int tj = lane & 15, tgi = (lane >> 4) & 1;
+    const int r = 4 * half + (tj >> 2);
+    const int sw = tile_swz<D>(r), sw8 = tile_swz<D>(r + 8);
+    const int chunk = tgi * 2 + ((tj & 3) >> 1), sub = (tj & 1) * 4;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      ta[dt][0] = base + (uint32_t)((r * D + sub + ((dt * 4 + chunk) ^ sw) * 8) * 2);
+      ta[dt][1] = base + (uint32_t)(((r + 8) * D + sub + ((dt * 4 + chunk) ^ sw8) * 8) * 2);
+      tg[dt][0] = ta[dt][0] + GB;
+      tg[dt][1] = ta[dt][1] + GB;
+    }
+  }
+  const uint32_t la = base + LB + half * 16;  // lse | delta of rows 4*half ..
 
-  // One 32-query block (tile rows mt*32 ..) against this wave's 32 keys.
-  auto block = [&](const bf16* ql, const bf16* gl, const float* sl, int g, int qb, int mt, auto edge_tag)
+  f32x16 s, dp;         // S and dP of the block in flight
+  u32x4 pd[2][2][2];    // [block parity][P | dS][16-query step]: bf16 pairs
+
+  // X: S = Q K^T and dP = dO V^T of block (ST, MT), MFMAs alternating.
+  auto X = [&](auto st_tag, auto mt_tag) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st_tag)::value, MT = decltype(mt_tag)::value;
+    constexpr int O = ST * TB + MT * 32 * D * 2;
+    bf16x8 qr[NK], gr[NK];
+    auto rd = [&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      ds_b128<O>(qr[j], ra[j]);
+      ds_b128<O>(gr[j], rg[j]);
+    };
+    static_for<0, kKvPf>(rd);
+    fence();
+    static_for<0, NK>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      if constexpr (j + kKvPf < NK) rd(std::integral_constant<int, j + kKvPf>{});
+      constexpr int ahead = 2 * (kKvPf < NK - 1 - j ? kKvPf : NK - 1 - j);
+      lgkm_tie<ahead + 1>(qr[j]);
+      if constexpr (j == 0)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qr[j], kf[j], f32x16{}, 0, 0, 0);
+      else
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qr[j], kf[j], s, 0, 0, 0);
+      lgkm_tie<ahead>(gr[j]);
+      if constexpr (j == 0)
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gr[j], vf[j], f32x16{}, 0, 0, 0);
+      else
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gr[j], vf[j], dp, 0, 0, 0);
+      fence();
+    });
+  };
+
+  // Y | V: dV^T += dO^T P and dK^T += Q^T dS of block (PS, PM) (P and dS in
+  // pd[PM]), with (VAL) the P / dS of block (ST, MT) -- from s and dp -- into
+  // pd[MT] between the MFMAs.  q0b: the block's first query; g: its head.
+  auto YV = [&](auto ps_tag, auto pm_tag, auto st_tag, auto mt_tag, auto edge_tag, auto val_tag, int q0b, int g)
       __attribute__((always_inline)) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    f32x16 s, dp;
+    constexpr int PS = decltype(ps_tag)::value, PM = decltype(pm_tag)::value;
+    constexpr int ST = decltype(st_tag)::value, MT = decltype(mt_tag)::value;
+    constexpr bool EDGE = decltype(edge_tag)::value, VAL = decltype(val_tag)::value;
+    // lse | delta of this lane's 16 rows of block (ST, MT): rows r*8 + 4*half + e.
+    f32x4 lq[4], dq4[4];
+    if constexpr (VAL) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(ql, mt, kk, l32, half, rsw), kf[kk], s, 0, 0, 0);
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_frag<D>(gl, mt, kk, l32, half, rsw), vf[kk], dp, 0, 0, 0);
-    bf16x8 pb[2], db[2];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int trow = mt * 32 + r * 8 + half * 4;  // tile row of entries 4r .. 4r+3
-      const f32x4 lse4 = *reinterpret_cast<const f32x4*>(&sl[trow]);
-      const f32x4 dl4 = *reinterpret_cast<const f32x4*>(&sl[kTile + trow]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = r * 4 + e;
-        const int q = qb + trow + e;
-        float x = s[i] * sl2;
-        if constexpr (MASK) {
-          if (q < Tq && key < Tk)
-            x += mask_log2(load_mask(p.mask, p.mask_dtype,
-                                    b * p.ms[0] + (int64_t)(hk * G + g) * p.ms[1] + (int64_t)q * p.ms[2] +
-                                        (int64_t)key * p.ms[3]));
-        }
-        float pr = __builtin_amdgcn_exp2f(x - lse4[e]);
-        if constexpr (EDGE) {
-          if (q >= Tq || (CAUSAL && key > q)) pr = 0.f;
-        }
-        const float ds = pr * (dp[i] - dl4[e]);
-        pb[i >> 3][i & 7] = static_cast<bf16>(pr);
-        db[i >> 3][i & 7] = static_cast<bf16>(ds);
+      for (int r = 0; r < 4; ++r) {
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(lq[r]) : "v"(la), "i"(ST * LS + (MT * 32 + r * 8) * 4));
+        asm volatile("ds_read_b128 %0, %1 offset:%2"
+                     : "=v"(dq4[r])
+                     : "v"(la), "i"(ST * LS + kTile * 4 + (MT * 32 + r * 8) * 4));
       }
     }
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr.read(gl, mt * 2 + ks, dt), pb[ks], dv[dt], 0, 0, 0);
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr.read(ql, mt * 2 + ks, dt), db[ks], dk[dt], 0, 0, 0);
-  };
-
-  auto step = [&](int t, const bf16* ql, const bf16* gl, const float* sl) __attribute__((always_inline)) {
-    const int g = tile_head(t), qb = tile_q(t) * kTile;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int q0r = qb + mt * 32;
-      if (q0r >= Tq || (CAUSAL && q0r + 31 < kw)) continue;  // no query of this block sees a key
-      const bool edge = (q0r + 32 > Tq) || (CAUSAL && q0r < kw + 31);
-      if (edge)
-        block(ql, gl, sl, g, qb, mt, std::true_type{});
+    // MFMA j: dV for j even, dK for j odd; d-block (j/2) % (D/32), step (j/2) / (D/32).
+    s16x4 tr[2 * NT][2];
+    auto rdt = [&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int m = j >> 1, dt = m % (D / 32), ks = m / (D / 32);
+      constexpr int O = PS * TB + (PM * 2 + ks) * 16 * D * 2;
+      if constexpr ((j & 1) == 0) {
+        ds_tr<O>(tr[j][0], tg[dt][0]);
+        ds_tr<O>(tr[j][1], tg[dt][1]);
+      } else {
+        ds_tr<O>(tr[j][0], ta[dt][0]);
+        ds_tr<O>(tr[j][1], ta[dt][1]);
+      }
+    };
+    static_for<0, kKvPf>(rdt);
+    fence();
+    static_for<0, 2 * NT>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int m = j >> 1, dt = m % (D / 32), ks = m / (D / 32);
+      if constexpr (j + kKvPf < 2 * NT) rdt(std::integral_constant<int, j + kKvPf>{});
+      lgkm_tie<2 * (kKvPf < 2 * NT - 1 - j ? kKvPf : 2 * NT - 1 - j)>(tr[j][0], tr[j][1]);
+      if constexpr (VAL && j == 0) {
+        // The lse / delta reads were issued before every operand read: the
+        // wait above covered them.
+        asm volatile("" : "+v"(lq[0]), "+v"(lq[1]), "+v"(lq[2]), "+v"(lq[3]));
+        asm volatile("" : "+v"(dq4[0]), "+v"(dq4[1]), "+v"(dq4[2]), "+v"(dq4[3]));
+      }
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(tr[j][0], tr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
+      if constexpr ((j & 1) == 0)
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pd[PM][0][ks]), dv[dt], 0, 0, 0);
       else
-        block(ql, gl, sl, g, qb, mt, std::false_type{});
-    }
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pd[PM][1][ks]), dk[dt], 0, 0, 0);
+      if constexpr (VAL) {
+        // Entry pairs (2k, 2k+1) of block (ST, MT), 8 over the 2*NT MFMAs.
+#pragma unroll
+        for (int k = j * 8 / (2 * NT); k < (j + 1) * 8 / (2 * NT); ++k) {
+          float sv[2] = {s[2 * k], s[2 * k + 1]}, dv2[2] = {dp[2 * k], dp[2 * k + 1]};
+          // Inputs taken here, so the work stays in this MFMA's slot.
+          asm volatile("" : "+v"(sv[0]), "+v"(sv[1]), "+v"(dv2[0]), "+v"(dv2[1]));
+          float pr[2], ds[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int i = 2 * k + u, r = i >> 2, e = i & 3;
+            const int q = q0b + r * 8 + half * 4 + e;
+            float x = sv[u] * sl2;
+            if constexpr (MASK) {
+              if (q < Tq && key < Tk)
+                x += mask_log2(load_mask(p.mask, p.mask_dtype,
+                                        b * p.ms[0] + (int64_t)(hk * G + g) * p.ms[1] + (int64_t)q * p.ms[2] +
+                                            (int64_t)key * p.ms[3]));
+            }
+            pr[u] = __builtin_amdgcn_exp2f(x - lq[r][e]);
+            if constexpr (EDGE) {
+              if (q >= Tq || (CAUSAL && key > q)) pr[u] = 0.f;
+            }
+            ds[u] = pr[u] * (dv2[u] - dq4[r][e]);
+          }
+          const bf16x2 wp = {static_cast<bf16>(pr[0]), static_cast<bf16>(pr[1])};
+          const bf16x2 wd = {static_cast<bf16>(ds[0]), static_cast<bf16>(ds[1])};
+          const uint32_t up = __builtin_bit_cast(uint32_t, wp), ud = __builtin_bit_cast(uint32_t, wd);
+          asm volatile("" ::"v"(up), "v"(ud));
+          pd[MT][0][k >> 2][k & 3] = up;
+          pd[MT][1][k >> 2][k & 3] = ud;
+        }
+      }
+      fence();
+    });
   };
 
-  wait_dma();
-  __syncthreads();
-  for (int t = 0; t < ntiles; t += 2) {
-    if (t + 1 < ntiles) issue(t + 1, q1, g1, st1);
-    step(t, q0, g0, st0);
+  // Block (ST, MT) of tile t after block (PS, PM): X, then Y | V.
+  auto step = [&](int t, auto ps_tag, auto pm_tag, auto st_tag, auto mt_tag) __attribute__((always_inline)) {
+    constexpr int MT = decltype(mt_tag)::value;
+    const int g = tile_head(t), q0b = tile_q(t) * kTile + MT * 32;
+    X(st_tag, mt_tag);
+    const bool edge = (q0b + 32 > Tq) || (CAUSAL && q0b < kw + 31);
+    if (edge)
+      YV(ps_tag, pm_tag, st_tag, mt_tag, std::true_type{}, std::true_type{}, q0b, g);
+    else
+      YV(ps_tag, pm_tag, st_tag, mt_tag, std::false_type{}, std::true_type{}, q0b, g);
+  };
+  // Tile t in stage ST, the previous tile in stage PS.
+  auto tile = [&](int t, auto st_tag, auto ps_tag) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st_tag)::value;
     wait_dma();
     __syncthreads();
-    if (t + 1 >= ntiles) break;
-    if (t + 2 < ntiles) issue(t + 2, q0, g0, st0);
-    step(t + 1, q1, g1, st1);
-    wait_dma();
-    __syncthreads();
+    // Stage (ST+1) % 3 last held tile t-2, whose last block's Y ran during
+    // tile t-1, before this barrier.
+    if (t + 1 < ntiles) issue(t + 1, (ST + 1) % kKvStages);
+    step(t, ps_tag, std::integral_constant<int, 1>{}, st_tag, std::integral_constant<int, 0>{});
+    step(t, st_tag, std::integral_constant<int, 0>{}, st_tag, std::integral_constant<int, 1>{});
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  if (ntiles > 0) {
+    // The first block's Y is a no-op: zero P / dS against tile 0's rows.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) pd[1][i][k] = u32x4{0u, 0u, 0u, 0u};
+    tile(0, I0{}, I0{});
+    for (int t = 1;; t += 3) {
+      if (t >= ntiles) break;
+      tile(t, I1{}, I0{});
+      if (t + 1 >= ntiles) break;
+      tile(t + 1, I2{}, I1{});
+      if (t + 2 >= ntiles) break;
+      tile(t + 2, I0{}, I2{});
+    }
+    // The last block's Y.
+    const int ls = (ntiles - 1) % kKvStages;
+    if (ls == 0)
+      YV(I0{}, I1{}, I0{}, I0{}, std::false_type{}, std::false_type{}, 0, 0);
+    else if (ls == 1)
+      YV(I1{}, I1{}, I0{}, I0{}, std::false_type{}, std::false_type{}, 0, 0);
+    else
+      YV(I2{}, I1{}, I0{}, I0{}, std::false_type{}, std::false_type{}, 0, 0);
   }
 
   if (key < Tk) {
