@@ -325,14 +325,14 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
           for (int u = 0; u < 2; ++u) {
             const int i = 2 * k + u, r = i >> 2, e = i & 3;
             const int q = q0b + r * 8 + half * 4 + e;
-            float x = sv[u] * sl2;
+            float x = fmaf(sv[u], sl2, -lq[r][e]);
             if constexpr (MASK) {
               if (q < Tq && key < Tk)
                 x += mask_log2(load_mask(p.mask, p.mask_dtype,
                                         b * p.ms[0] + (int64_t)(hk * G + g) * p.ms[1] + (int64_t)q * p.ms[2] +
                                             (int64_t)key * p.ms[3]));
             }
-            pr[u] = __builtin_amdgcn_exp2f(x - lq[r][e]);
+            pr[u] = __builtin_amdgcn_exp2f(x);
             if constexpr (EDGE) {
               if (q >= Tq || (CAUSAL && key > q)) pr[u] = 0.f;
             }
