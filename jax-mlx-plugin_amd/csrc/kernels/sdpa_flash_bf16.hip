@@ -300,7 +300,9 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 bool flash_bf16_supports(const SdpaParams& p) {
   if (p.dtype != MFX_BF16) return false;
   if (!(p.scale_log2 > 0.f)) return false;  // the exp2 FMA folds a positive scale
-  // Buffer-resource offsets of one head's K/V rows are 31-bit.
+  // K/V rows are read through one buffer resource per head spanning its Tk
+  // rows, range-checked on 31-bit lane offsets: non-negative row strides only.
+  if (p.ks[2] < 0 || p.vs[2] < 0) return false;
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;

@@ -67,6 +67,28 @@ def test_kernel_selection_per_config(native):
     assert native.sdpa_kernel_name(q, k, v) == "generic"
 
 
+def test_negative_kv_row_strides_leave_buffer_resource_kernels(native):
+    """The bf16 flash and MFMA decode kernels read K/V through buffer
+    resources spanning a head's Tk rows, range-checked on forward offsets:
+    K/V views with negative row strides (possible through the C ABI) must
+    select a kernel that addresses K/V with plain pointers instead (the
+    shape-general kernel, or for decode the vector-ALU split-KV kernel)."""
+    import ctypes
+
+    import torch
+
+    lib = native.load()
+    for qs, ks, want, fallback in (((1, 4, 256, 128), (1, 4, 256, 128), "flash_bf16_d128", "generic"),
+                                   ((2, 8, 1, 128), (2, 2, 1000, 128), "decode_splitkv_mfma", "decode_splitkv")):
+        q, k = _cpu_tensors(torch, qs, ks)
+        assert native.sdpa_kernel_name(q, k, k) == want
+        a = native.sdpa_args(q, k, k, q)
+        a.k_strides[2] = -a.k_strides[2]
+        a.v_strides[2] = -a.v_strides[2]
+        got = lib.mfx_sdpa_kernel_name(ctypes.byref(a)).decode()
+        assert got == fallback, got
+
+
 def test_decode_workspace_is_sized(native):
     import torch
 
