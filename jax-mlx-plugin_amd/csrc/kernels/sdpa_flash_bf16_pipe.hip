@@ -28,9 +28,12 @@
 // its own for the LDS-DMA into the other stage.  sched_barrier fences keep
 // this interleave as written.
 //
-// A wavefront's last tile also computes S of the K stage behind it (and the
-// exp2 of half of it); that S is never used, which keeps one code path in
-// the loop and the register allocation spill-free.
+// A wavefront's last tile runs outside the loop (tile_last: no S of a next
+// tile), its registers moved to the even-tile set and its V stage a runtime
+// offset, so the loop keeps its two tile bodies and the kernel stays
+// spill-free.  No spill is allowed here: the inline-asm LDS reads complete
+// after the asm statement, and a spill or copy of a destination register
+// placed before its lgkmcnt wait would save the value before it arrives.
 #include <type_traits>
 
 #include "sdpa_tiles.h"
@@ -359,6 +362,37 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       fence();
     });
   };
+  // A wavefront's last tile t: no S(t+1) and no exp2 of it; the exp2 of keys
+  // 32-63 of S(t), the row-sum check and the PV(t) MFMAs as in tile().
+  auto tile_last = [&](f32x16 (&sc)[2], u32x4 (&pc)[2], int vs_bytes) {
+    s16x4 vr[MP][2];
+    auto rdv = [&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      ds_tr<2 * TB + ks * 16 * D * 2>(vr[j][0], va[dt][0] + vs_bytes);
+      ds_tr<2 * TB + ks * 16 * D * 2>(vr[j][1], va[dt][1] + vs_bytes);
+    };
+    static_for<0, kPfV>(rdv);
+    fence();
+    float ls = 0.f;
+#pragma unroll
+    for (int g = 8; g < 16; ++g) exp_pair(sc, g, pb, ls);
+    float lt = lf + ls;
+    if (__builtin_amdgcn_ballot_w64(!(lt <= kSumCap))) lt = rebase(sc, pc);
+    l_run += lt;
+    lf = 0.f;
+    static_for<0, MP>([&](auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      if constexpr (j + kPfV < MP) rdv(std::integral_constant<int, j + kPfV>{});
+      lgkm_tie<wait_v(j, MP)>(vr[j][0], vr[j][1]);
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
+      const u32x4 pbk = ks < 2 ? pc[ks & 1] : pb[ks & 1];
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pbk), o[dt], 0, 0, 0);
+      fence();
+    });
+  };
 
   wait_dma();
   __syncthreads();
@@ -374,19 +408,45 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   // Iteration t: K(t+1) in K stage (t+1)&1, V(t) in V stage t&1; loads K(t+2)
   // into K stage t&1 and V(t+1) into V stage (t+1)&1, whose previous tiles
   // every wavefront has finished reading at the barrier.
-  auto iter = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pc)[2], u32x4 (&pn)[2], auto par_tag) {
-    constexpr int PAR = decltype(par_tag)::value;  // t & 1
+  // Every wavefront passes N barriers: tiles 0 .. nw-2 in the pipelined
+  // loop, tile nw-1 by tile_last, then barrier-only iterations that keep
+  // issuing the workgroup's loads.
+  auto sync_load = [&](int t) {
     wait_dma();
     __syncthreads();
-    if (t + 2 < N) kload.load(t + 2, kst[PAR], wave);
-    if (t + 1 < N) vload.load(t + 1, vst[PAR ^ 1], wave);
-    if (t < nw) tile(sc, sn, pc, pn, t, std::integral_constant<int, PAR ^ 1>{}, std::integral_constant<int, PAR>{});
+    if (t + 2 < N) kload.load(t + 2, (t & 1) ? kst[1] : kst[0], wave);
+    if (t + 1 < N) vload.load(t + 1, (t & 1) ? vst[0] : vst[1], wave);
   };
-  for (int t = 0; t < N; t += 2) {
-    iter(t, s0, s1, pf0, pf1, std::integral_constant<int, 0>{});
-    if (t + 1 >= N) break;
-    iter(t + 1, s1, s0, pf1, pf0, std::integral_constant<int, 1>{});
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  int last = -1;
+  for (int t = 0; t < nw; t += 2) {
+    if (t + 1 >= nw) {
+      last = t;
+      break;
+    }
+    sync_load(t);
+    tile(s0, s1, pf0, pf1, t, I1{}, I0{});
+    if (t + 2 >= nw) {
+      last = t + 1;
+      break;
+    }
+    sync_load(t + 1);
+    tile(s1, s0, pf1, pf0, t + 1, I0{}, I1{});
   }
+  int t = 0;
+  if (last >= 0) {
+    if (last & 1) {
+      s0[0] = s1[0];
+      s0[1] = s1[1];
+      pf0[0] = pf1[0];
+      pf0[1] = pf1[1];
+    }
+    sync_load(last);
+    tile_last(s0, pf0, (last & 1) * TB);
+    t = last + 1;
+  }
+  for (; t < N; ++t) sync_load(t);
 
   const float lt = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / lt;
