@@ -484,7 +484,7 @@ const char* mfx_gemm_kernel_name(const mfx_gemm_args* args);
  * ignored): C is never stored.  The program's output index space must be C's
  * [batch * m, n] (rank-1..8 dims whose trailing dims span exactly n) with a
  * contiguous output aligned to two elements; gemm must be an f32 row-major
- * product the tile kernel handles (no transposes, k % 4 == 0, even n, lda and
+ * product the tile kernel handles (no transposes, k % 4 == 0, n % 4 == 0, lda and
  * ldb multiples of 4 -- so n % 4 == 0 for a contiguous B -- A and B 16-byte
  * aligned, ldc = n, stride_c = m * n).  The kernel is generated from the program and compiled
  * with hipRTC for gfx950 on first use (cached per device and program); the

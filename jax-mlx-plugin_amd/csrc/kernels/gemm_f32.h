@@ -17,7 +17,7 @@ constexpr int kGemmF32Stages = 2;
 constexpr int kGemmF32MinBlocks = 3;
 
 // True when the tile kernel handles `a`: f32 in and out, row-major A[m][k]
-// and B[k][n], K % 4 == 0, even N, leading dims and batch strides that keep
+// and B[k][n], K % 4 == 0, N % 4 == 0, leading dims and batch strides that keep
 // A and B rows 16-byte aligned, and 32-bit load offsets.
 bool gemm_f32_supported(const mfx_gemm_args& a);
 

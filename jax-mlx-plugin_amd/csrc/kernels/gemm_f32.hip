@@ -23,7 +23,7 @@ bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p)
 bool gemm_f32_supported(const mfx_gemm_args& a) {
   if (a.dtype != MFX_F32 || a.c_dtype != MFX_F32 || a.trans_a || a.trans_b) return false;
   if (a.batch < 1 || a.batch > 65535 || a.m < 1 || a.n < 1 || a.k < 0) return false;
-  if (a.k % 4 || a.n % 2 || a.lda % 4 || a.ldb % 4 || a.ldc % 2) return false;
+  if (a.k % 4 || a.n % 4 || a.lda % 4 || a.ldb % 4 || a.ldc % 2) return false;
   if (a.lda < a.k || a.ldb < a.n || a.ldc < a.n) return false;
   if (a.stride_a % 4 || a.stride_b % 4 || a.stride_c % 2) return false;
   if (!aligned(a.a, 16) || !aligned(a.b, 16) || !aligned(a.c, 8)) return false;

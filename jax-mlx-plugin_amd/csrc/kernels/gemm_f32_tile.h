@@ -26,10 +26,15 @@
 //   reads of the next tile) sits halfway through the last group's MFMAs.
 // Out-of-range reads come back as zeros (buffer range checks): rows past M,
 // k-rows of B past K; A chunks past K are pointed out of range explicitly.
-// Columns past N are computed from whatever the loads return and never
-// stored.
+// The hardware checks only the per-lane (VGPR) offset of a raw buffer load
+// against the resource's extent, not the scalar offset, so every row step
+// lives in the per-lane offset and the k-tile position moves the resource
+// base (its extent shrinking by the same amount): no load can reach past
+// A's first min(M - m0, BM) rows of the tile or past B's last element,
+// B[K-1][N-1].  Columns past N are computed from whatever the loads return
+// (elements of B's next row, or zeros on its last row) and never stored.
 //
-// Requirements checked by the host: K % 4 == 0, N % 2 == 0, lda and ldb
+// Requirements checked by the host: K % 4 == 0, N % 4 == 0, lda and ldb
 // multiples of 4, A and B 16-byte aligned, C 8-byte aligned, and the byte
 // offsets a k-tile load forms (BM * lda * 4, K * ldb * 4) below 2^31.
 #pragma once
@@ -133,32 +138,46 @@ __device__ __forceinline__ void gemm_tile(const Params& p, const typename E::Arg
   const float* B = p.b + (long long)bz * p.sb;
 
   // A loader: instruction i of wave w fills rows (i*NW + w)*A_ROWS + lane/8,
-  // chunk slot lane%8 from source chunk slot ^ swz(row).
-  const long long a_rem = (long long)(p.M - m0) * p.lda * 4;
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A + (long long)m0 * p.lda), (short)0, (int)(a_rem > 0x7fffffffLL ? 0x7fffffffLL : a_rem), 0x00020000);
+  // chunk slot lane%8 from source chunk slot ^ swz(row).  The resource of
+  // k-tile t starts at A[m0][t*kBK] and spans the tile's rows below M
+  // (a_span bytes from A[m0][0]) minus that start.
+  const int a_rows = p.M - m0 < BM ? p.M - m0 : BM;
+  const int a_span = a_rows * p.lda * 4;
+  const char* a_base = (const char*)(A + (long long)m0 * p.lda);
   const int a_row = wave * A_ROWS + lane / 8;
   const int a_chunk = (lane & 7) ^ swz(a_row);
-  const unsigned a_vo = (unsigned)((a_row * p.lda + a_chunk * 4) * 4);
-  // B loader: instruction i of wave w fills k-rows (i*NW + w)*B_ROWS + lane/(BN/4).
-  const __amdgpu_buffer_rsrc_t rb =
-      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((long long)p.K * p.ldb * 4), 0x00020000);
+  unsigned a_vo[A_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i)
+    a_vo[i] = (unsigned)(((i * NW * A_ROWS + a_row) * p.lda + a_chunk * 4) * 4);
+  // B loader: instruction i of wave w fills k-rows (i*NW + w)*B_ROWS + lane/(BN/4);
+  // the resource of k-tile t starts at B[t*kBK][0] and ends at B's last
+  // element (N % 4 == 0, so no 16-byte load straddles that end).
+  const int b_span = ((p.K - 1) * p.ldb + p.N) * 4;
   const int b_row = wave * B_ROWS + lane / (BN / 4);
-  const unsigned b_vo = (unsigned)((b_row * p.ldb + n0 + (lane % (BN / 4)) * 4) * 4);
+  unsigned b_vo[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < B_LOADS; ++i)
+    b_vo[i] = (unsigned)((((i * NW * B_ROWS + b_row) * p.ldb) + n0 + (lane % (BN / 4)) * 4) * 4);
   const int T = (p.K + kBK - 1) / kBK;
 
   auto issue = [&](int t, int stage) {
     char* sa = smem + stage * STAGE;
     char* sb = sa + A_BYTES;
-    const unsigned avo = t * kBK + a_chunk * 4 < p.K ? a_vo : 0x80000000u;
+    const bool a_in = t * kBK + a_chunk * 4 < p.K;
+    const int a_off_t = t * kBK * 4, b_off_t = t * kBK * p.ldb * 4;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a_base + a_off_t), (short)0, a_span - a_off_t, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)((const char*)B + b_off_t), (short)0, b_span - b_off_t, 0x00020000);
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa + (i * NW + wave) * 1024), 16, avo,
-                                               i * NW * A_ROWS * p.lda * 4 + t * kBK * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa + (i * NW + wave) * 1024), 16,
+                                               a_in ? a_vo[i] : 0x80000000u, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb + (i * NW + wave) * 1024), 16, b_vo,
-                                               (i * NW * B_ROWS + t * kBK) * p.ldb * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb + (i * NW + wave) * 1024), 16, b_vo[i], 0,
+                                               0, 0);
   };
 
   const int wm0 = (wave / (BN / kWN)) * kWM, wn0 = (wave % (BN / kWN)) * kWN;

@@ -654,6 +654,9 @@ bool bwd_mfma_supports(const SdpaBwdParams& p) {
     if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.dos[i] % 8 || p.dqs[i] % 4 || p.dks[i] % 4 ||
         p.dvs[i] % 4 || p.os[i] % 8)
       return false;
+  // K / V / Q / dO rows are read through buffer resources whose extents
+  // assume rows of at least D elements (rows past the end then read zeros).
+  if (p.ks[2] < p.D || p.vs[2] < p.Dv || p.qs[2] < p.D || p.dos[2] < p.Dv) return false;
   // Buffer-resource extents are 31-bit: one kv head's K / V rows, and the
   // query rows (and lse / delta) of all heads of one group.
   const int64_t lim = 1LL << 31;

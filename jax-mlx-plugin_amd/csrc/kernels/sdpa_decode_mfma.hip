@@ -783,7 +783,8 @@ bool decode_mfma_supports(const SdpaParams& p) {
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (p.group * p.Tq > 32) return false;
   if ((int64_t)p.B * p.Hkv * ((p.Tk + kDN - 1) / kDN) >= (1LL << 31)) return false;  // tile lists
-  if (p.ks[2] < 0 || p.vs[2] < 0) return false;  // buffer-resource extents span forward rows
+  // Buffer-resource extents span Tk forward rows of at least D elements each.
+  if (p.ks[2] < p.D || p.vs[2] < p.Dv) return false;
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v)) return false;
   for (int i = 0; i < 3; ++i)

@@ -301,8 +301,11 @@ bool flash_bf16_supports(const SdpaParams& p) {
   if (p.dtype != MFX_BF16) return false;
   if (!(p.scale_log2 > 0.f)) return false;  // the exp2 FMA folds a positive scale
   // K/V rows are read through one buffer resource per head spanning its Tk
-  // rows, range-checked on 31-bit lane offsets: non-negative row strides only.
-  if (p.ks[2] < 0 || p.vs[2] < 0) return false;
+  // rows, range-checked on 31-bit lane offsets: row strides of at least D
+  // (rows past Tk then start at or past the extent and read as zeros; a
+  // smaller stride, such as 0 for a broadcast view, would leave rows past Tk
+  // inside it and the last row's tail outside).
+  if (p.ks[2] < p.D || p.vs[2] < p.Dv) return false;
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;

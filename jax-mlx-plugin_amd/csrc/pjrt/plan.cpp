@@ -1262,7 +1262,10 @@ class Planner {
   // (a training step's attention and its gradient): the forward also writes
   // its row log-sum-exp, and the backward reads it and the forward's output
   // instead of recomputing both (same forward kernel, so the same bits).
+  // Several backward steps of one forward (two VJPs with different
+  // cotangents, a Jacobian) share the one lse value that forward writes.
   void link_sdpa_backward() {
+    std::map<size_t, int> fwd_lse;  // forward step index -> its lse value
     for (auto& bw : sdpa_bwd_meta_) {
       const SdpaBwdMeta& m = bw.second;
       const mfx_sdpa_bwd_args& ba = m.a;
@@ -1292,10 +1295,19 @@ class Planner {
         for (int i = 0; i < 4; ++i) probe.fwd_out_strides[i] = fa.o_strides[i];
         const size_t ws = mfx_sdpa_bwd_workspace_size(&probe);
         if (!ws) continue;
-        Type lt;
-        lt.dtype = DType::kF32;
-        lt.dims = {fa.B * fa.Hq * fa.Tq};
-        const int lse = new_temp(lt);
+        int lse;
+        auto linked = fwd_lse.find(fw.first);
+        if (linked != fwd_lse.end()) {
+          lse = linked->second;
+        } else {
+          Type lt;
+          lt.dtype = DType::kF32;
+          lt.dims = {fa.B * fa.Hq * fa.Tq};
+          lse = new_temp(lt);
+          fwd_lse[fw.first] = lse;
+          plan_.steps_[fw.first] = sdpa_step(f, lse);
+          io_[fw.first].writes.push_back(lse);
+        }
         Type wt;
         wt.dtype = DType::kU8;
         wt.dims = {(int64_t)ws};
@@ -1306,8 +1318,6 @@ class Planner {
         mb.a.fwd_out_strides[3] = fa.o_strides[3];
         mb.ws_v = new_temp(wt);
         mb.ws = ws;
-        plan_.steps_[fw.first] = sdpa_step(f, lse);
-        io_[fw.first].writes.push_back(lse);
         plan_.steps_[bw.first] = sdpa_bwd_step(mb, f.out_v, lse);
         io_[bw.first] = StepIO{{mb.q, mb.k, mb.v, mb.g, f.out_v, lse}, {mb.dq, mb.dk, mb.dv, mb.ws_v}};
         break;
@@ -1616,6 +1626,12 @@ class Planner {
       // Values never read or written by a step (unused) stay unplaced.
     }
     plan_.arena_bytes_ = (size_t)top;
+    for (size_t s = 0; s < io_.size() && s < plan_.steps_.size(); ++s) {
+      plan_.steps_[s].reads.clear();
+      plan_.steps_[s].writes.clear();
+      for (int v : io_[s].reads) plan_.steps_[s].reads.push_back(resolve_alias(v));
+      for (int v : io_[s].writes) plan_.steps_[s].writes.push_back(resolve_alias(v));
+    }
     // Every value a step touches must be placed.
     for (auto& io : io_)
       for (auto* vec : {&io.reads, &io.writes})
@@ -1772,8 +1788,17 @@ std::string Plan::summary_json() const {
   std::ostringstream o;
   o << "{\"arena_bytes\": " << arena_bytes_ << ", \"steps\": [";
   for (size_t i = 0; i < steps_.size(); ++i)
+  {
     o << (i ? ", " : "") << "{\"kind\": \"" << steps_[i].kind << "\", \"label\": \"" << steps_[i].label
-      << "\", \"flops\": " << steps_[i].flops << "}";
+      << "\", \"flops\": " << steps_[i].flops;
+    for (int w = 0; w < 2; ++w) {
+      const std::vector<int>& vs = w ? steps_[i].writes : steps_[i].reads;
+      o << (w ? ", \"writes\": [" : ", \"reads\": [");
+      for (size_t j = 0; j < vs.size(); ++j) o << (j ? ", " : "") << vs[j];
+      o << "]";
+    }
+    o << "}";
+  }
   o << "]}";
   return o.str();
 }

@@ -41,6 +41,7 @@ struct Step {
   std::string label;  // op / kernel detail
   double flops = 0;
   double bytes = 0;
+  std::vector<int> reads, writes;  // value ids the step reads / writes (aliases resolved), for inspection
   // Resolves pointers and launches; returns MFX_OK or an error code.
   std::function<int(const ExecBuffers&, std::string&)> run;
 };

@@ -478,28 +478,38 @@ def custom_call_sdpa_bwd_module(B=2, T=64, N=4, K=None, H=64, S=None, dt="f32", 
     return module("jit_mlx_sdpa_bwd", [f.text([f"{r}#0", f"{r}#1", f"{r}#2"], [qt, kt, kt])])
 
 
-def sdpa_vjp_module(B=2, T=64, N=4, K=None, H=64, S=None, dt="f32", scale=0.125, same_inputs=True):
+def sdpa_vjp_module(B=2, T=64, N=4, K=None, H=64, S=None, dt="f32", scale=0.125, same_inputs=True,
+                    cotangents=1):
     """jax.vjp of the reference's mlx_dot_product_attention (custom_vjp:
     src/jax_mlx/sdpa.py:156-191) inside one jit: custom_call @mlx_sdpa on
     (q, k, v), then @mlx_sdpa_bwd on the saved (q, k, v) and the cotangent
     g.  Results: the attention output and (dq, dk, dv).  same_inputs=False
     feeds the backward q + 0 from a separate argument instead (a different
-    q value)."""
+    q value).  cotangents=2 applies the VJP to a second cotangent (the last
+    argument) as well, appending its (dq, dk, dv): two backward steps of one
+    forward, as a Jacobian makes."""
     K = K or N
     S = S or T
     qt, kt = ty([B, T, N, H], dt), ty([B, S, K, H], dt)
     args = [([B, T, N, H], dt), ([B, S, K, H], dt), ([B, S, K, H], dt), ([B, T, N, H], dt)]
     if not same_inputs:
         args.append(([B, T, N, H], dt))
+    if cotangents == 2:
+        args.append(([B, T, N, H], dt))
     f = Fn("main", args)
     cfg = '{\\22scale\\22: ' + repr(float(scale)) + '}'
     o = f.emit(f'stablehlo.custom_call @mlx_sdpa(%arg0, %arg1, %arg2) {{backend_config = "{cfg}"}} : '
                f"({qt}, {kt}, {kt}) -> {qt}")
     qb = "%arg0" if same_inputs else "%arg4"
-    r = f.new()
-    f.lines.append(f'    {r}:3 = stablehlo.custom_call @mlx_sdpa_bwd({qb}, %arg1, %arg2, %arg3) '
-                   f'{{backend_config = "{cfg}"}} : ({qt}, {kt}, {kt}, {qt}) -> ({qt}, {kt}, {kt})')
-    return module("jit_mlx_sdpa_vjp", [f.text([o, f"{r}#0", f"{r}#1", f"{r}#2"], [qt, qt, kt, kt])])
+    res, rts = [o], [qt]
+    for c in range(cotangents):
+        g = "%arg3" if c == 0 else f"%arg{len(args) - 1}"
+        r = f.new()
+        f.lines.append(f'    {r}:3 = stablehlo.custom_call @mlx_sdpa_bwd({qb}, %arg1, %arg2, {g}) '
+                       f'{{backend_config = "{cfg}"}} : ({qt}, {kt}, {kt}, {qt}) -> ({qt}, {kt}, {kt})')
+        res += [f"{r}#0", f"{r}#1", f"{r}#2"]
+        rts += [qt, kt, kt]
+    return module("jit_mlx_sdpa_vjp", [f.text(res, rts)])
 
 
 def custom_call_layer_norm_bwd_module(shape=(4, 512), eps=1e-5, dt="f32", pdt=None):

@@ -84,6 +84,25 @@ def test_gemm_tile_batched_and_strided(torch, nt):
     _check_gemm(torch, nt, big_a[:, :64], big_b[:, 32:128], "gemm_f32_tile")
 
 
+@pytest.mark.parametrize("m,n,k", [(65, 128, 36), (65, 4, 36), (1, 128, 4096), (97, 8, 68)])
+def test_gemm_tile_reads_nothing_past_its_operands(torch, nt, m, n, k):
+    """A and B each end where a NaN-filled guard region of their allocation
+    begins.  Rows past M of the last row tile and k-rows past K of the last
+    k-tile must read as zeros (buffer range checks), never the guard: one
+    NaN read would reach every output of its tile (0 * NaN).  M % 64 in
+    1..32 and K % 32 != 0 make both happen."""
+    g = torch.Generator(device="cpu").manual_seed(m + n + k)
+    guard = 1 << 20
+    fa = torch.full((m * k + guard,), float("nan"), dtype=torch.float32)
+    fb = torch.full((k * n + guard,), float("nan"), dtype=torch.float32)
+    fa[: m * k] = torch.randn(m * k, generator=g)
+    fb[: k * n] = torch.randn(k * n, generator=g) / k ** 0.5
+    fa, fb = fa.cuda(), fb.cuda()
+    a, b = fa[: m * k].view(m, k), fb[: k * n].view(k, n)
+    out = _check_gemm(torch, nt, a, b, "gemm_f32_tile")
+    assert torch.isfinite(out).all()
+
+
 def test_gemm_outside_tile_rules_goes_to_rocblas(torch, nt):
     """A rows off 16-byte alignment, and B rows of 130 floats (ldb % 4 != 0):
     rocBLAS, to the same bar."""

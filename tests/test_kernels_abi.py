@@ -89,6 +89,34 @@ def test_negative_kv_row_strides_leave_buffer_resource_kernels(native):
         assert got == fallback, got
 
 
+def test_short_kv_row_strides_leave_buffer_resource_kernels(native):
+    """K/V row strides below D (0 for a broadcast view such as
+    torch.expand, or rows that overlap) leave rows past Tk inside a buffer
+    resource spanning Tk rows: the bf16 flash, MFMA decode and MFMA backward
+    kernels must not take them (shape-general kernel, VALU split-KV decode,
+    generic backward)."""
+    import ctypes
+
+    import torch
+
+    lib = native.load()
+    for qs, ks, want, fallback in (((1, 4, 256, 128), (1, 4, 256, 128), "flash_bf16_d128", "generic"),
+                                   ((2, 8, 1, 128), (2, 2, 1000, 128), "decode_splitkv_mfma", "decode_splitkv")):
+        for stride in (0, 64):
+            for which in ("k", "v"):
+                q, k = _cpu_tensors(torch, qs, ks)
+                a = native.sdpa_args(q, k, k, q)
+                getattr(a, which + "_strides")[2] = stride
+                got = lib.mfx_sdpa_kernel_name(ctypes.byref(a)).decode()
+                assert got == fallback, (which, stride, got)
+    q, k = _cpu_tensors(torch, (1, 4, 256, 128), (1, 4, 256, 128))
+    assert native.sdpa_bwd_kernel_name(q, k, k) == "mfma_bf16_d128"
+    for which in ("k", "v"):
+        a = native.sdpa_bwd_args(q, k, k, q, q, k, k)
+        getattr(a, which + "_strides")[2] = 0
+        assert lib.mfx_sdpa_bwd_kernel_name(ctypes.byref(a)).decode() == "generic", which
+
+
 def test_decode_workspace_is_sized(native):
     import torch
 

@@ -335,14 +335,29 @@ def test_sdpa_bf16_golden(cuda, nat, golden):
     check_sdpa(out, golden["sdpa_bf16_out_causal"], "bf16")
 
 
+# (batch, head) pairs of config 3 checked against the oracle at full size.
+# The prefill kernels deal (batch*Hq + head) = bh to XCD bh % 8, slot
+# (bh / 8) % 4 of a four-head group, group bh / 32: these eight cover every
+# XCD residue, every group slot twice and every group twice.
+CONFIG3_BH = [0, 9, 50, 59, 68, 77, 118, 127]
+CONFIG3_HEADS = [(bh // 32, bh % 32) for bh in CONFIG3_BH]
+
+
+def test_config3_heads_cover_every_xcd_and_slot():
+    assert sorted(bh % 8 for bh in CONFIG3_BH) == list(range(8))
+    assert sorted((bh // 8) % 4 for bh in CONFIG3_BH) == [0, 0, 1, 1, 2, 2, 3, 3]
+    assert sorted(bh // 32 for bh in CONFIG3_BH) == [0, 0, 1, 1, 2, 2, 3, 3]
+
+
 def test_sdpa_bf16_config3_full_size(cuda, nat, oracle):
-    """B4/H32/T2048/d128 causal bf16: two whole heads against the oracle,
-    plus size-independent properties on every head."""
+    """B4/H32/T2048/d128 causal bf16: eight whole heads (one per XCD residue
+    and group slot of the kernel's block mapping) against the oracle, plus
+    size-independent properties on every head."""
     q, k, v = make_qkv(cuda, 3, (4, 32, 2048, 128), (4, 32, 2048, 128), cuda.bfloat16)
     assert nat.sdpa_kernel_name(q, k, v, causal=True) == "flash_bf16_d128"
     out = nat.sdpa(q, k, v, scale=128 ** -0.5, causal=True)
     cuda.cuda.synchronize()
-    for b, h in ((0, 0), (3, 31)):
+    for b, h in CONFIG3_HEADS:
         ref = oracle.sdpa(host(q[b:b + 1, h:h + 1]), host(k[b:b + 1, h:h + 1]),
                           host(v[b:b + 1, h:h + 1]), 128 ** -0.5, causal=True)
         check_sdpa(out[b:b + 1, h:h + 1], ref, "bf16")
@@ -356,6 +371,29 @@ def test_sdpa_bf16_config3_full_size(cuda, nat, oracle):
     slack = 1e-2 * vf.abs().max()
     assert bool(((of <= hi + slack) & (of >= lo - slack)).all())
     assert bool(cuda.isfinite(of).all())
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("which", ["k", "v"])
+def test_sdpa_broadcast_kv_rows(cuda, nat, oracle, dtype, which):
+    """K or V as a broadcast view (row stride 0, torch.expand): the buffer-
+    resource kernels do not take it (their extents assume rows of at least
+    D elements) and the kernel that does matches the oracle.  With V
+    broadcast every output row is that one V row (the weights sum to 1)."""
+    td = cuda.float32 if dtype == "f32" else cuda.bfloat16
+    q, k, v = make_qkv(cuda, 31, (2, 4, 96, 64), (2, 4, 96, 64), td)
+    if which == "v":
+        v = v[:, :, :1].expand(2, 4, 96, 64)
+    else:
+        k = k[:, :, :1].expand(2, 4, 96, 64)
+    name = nat.sdpa_kernel_name(q, k, v)
+    assert name.startswith("flash_f32") if dtype == "f32" else name == "generic", name
+    out = nat.sdpa(q, k, v, scale=0.125)
+    ref = oracle.sdpa(host(q), host(k), host(v), 0.125)
+    check_sdpa(out, ref, dtype)
+    if which == "v":
+        err = float(np.abs(host(out) - host(v)).max())
+        assert err <= (1e-5 if dtype == "f32" else 1e-2), err
 
 
 def test_sdpa_gqa_decode_golden(cuda, nat, golden):
@@ -667,9 +705,10 @@ def test_sdpa_bwd_kernel_selection(cuda, nat):
 
 
 def test_sdpa_bwd_config3_full_size(cuda, nat, oracle):
-    """Config 3 shape (bf16 [4,32,2048,128], causal): the gradients of two
-    (batch, head) pairs against the fp64 oracle run on those heads alone
-    (heads are independent), plus finiteness everywhere."""
+    """Config 3 shape (bf16 [4,32,2048,128], causal): the gradients of eight
+    (batch, head) pairs (one per XCD residue and group slot) against the
+    fp64 oracle run on those heads alone (heads are independent), plus
+    finiteness everywhere."""
     q, k, v = make_qkv(cuda, 3, (4, 32, 2048, 128), (4, 32, 2048, 128), cuda.bfloat16)
     g = dev(cuda, np.random.default_rng(103).standard_normal((4, 32, 2048, 128)), cuda.bfloat16)
     assert nat.sdpa_bwd_kernel_name(q, k, v, causal=True) == "mfma_bf16_d128"
@@ -678,7 +717,7 @@ def test_sdpa_bwd_config3_full_size(cuda, nat, oracle):
     for t in (dq, dk, dv):
         assert bool(cuda.isfinite(t).all())
     sc = 1.0 / np.sqrt(128)
-    for b, h in ((0, 0), (3, 31)):
+    for b, h in CONFIG3_HEADS:
         sl = lambda t: host(t[b:b + 1, h:h + 1])
         refs = oracle.sdpa_bwd(sl(q), sl(k), sl(v), sl(g), sc, causal=True)
         for name, o, r in zip(("dq", "dk", "dv"), (dq, dk, dv), refs):

@@ -424,6 +424,19 @@ def test_sdpa_vjp_links_forward_and_backward(api):
     assert d["plan"]["arena_bytes"] < d2["plan"]["arena_bytes"]
 
 
+def test_sdpa_vjp_two_cotangents_share_the_forward_lse(api):
+    """Two backward steps of one forward (a VJP applied to two cotangents):
+    the forward writes one lse value and both backward steps read that
+    value (a second lse temp would be written by nobody)."""
+    d = api.inspect(M.sdpa_vjp_module(cotangents=2))
+    st = d["plan"]["steps"]
+    assert [s["label"] for s in st] == ["sdpa (+ lse)"] + ["mfx.sdpa_bwd (forward's out and lse)"] * 2
+    fw_out, lse = st[0]["writes"]
+    for bw in st[1:]:
+        assert fw_out in bw["reads"] and lse in bw["reads"]
+    assert sum(lse in s["writes"] for s in st) == 1
+
+
 @pytest.mark.parametrize("epilogue", ["bias", "bias_gelu", "bias_residual"])
 def test_dense_epilogue_fuses_into_gemm(api, epilogue):
     """A dot_general whose only reader is one elementwise program at the

@@ -525,6 +525,26 @@ def test_sdpa_vjp_module_linked(client, dt):
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_sdpa_vjp_two_cotangents(client, dt):
+    """Two backward steps of one forward (the VJP applied to two
+    cotangents): both read the lse the forward writes.  Each (dq, dk, dv)
+    equals the single-cotangent module's recomputing path (backward on a
+    separate, equal q argument) for that cotangent, bit for bit."""
+    rng = np.random.default_rng(43)
+    B, T, N, H = 2, 128, 4, 64
+    q, k, v, g1, g2 = (rng.standard_normal((B, T, N, H)).astype(np.float32) for _ in range(5))
+    if dt == "bf16":
+        q, k, v, g1, g2 = (bf16_round(a) for a in (q, k, v, g1, g2))
+    both = run(client, M.sdpa_vjp_module(B=B, T=T, N=N, H=H, dt=dt, cotangents=2), [q, k, v, g1, g2], [dt] * 5)
+    for g, got in ((g1, both[1:4]), (g2, both[4:7])):
+        plain = run(client, M.sdpa_vjp_module(B=B, T=T, N=N, H=H, dt=dt, same_inputs=False), [q, k, v, g, q],
+                    [dt] * 5)
+        assert np.array_equal(both[0], plain[0])
+        for a, b in zip(got, plain[1:]):
+            assert np.array_equal(a, b)
+
+
 def test_escaping_intermediates_layer_norm(client, oracle):
     """Escape guard (reference src/jax_mlx_pjrt.cpp:1843-1855): a LayerNorm
     whose mean and variance are also results.  The fusion fires and the
