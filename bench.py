@@ -227,7 +227,7 @@ def bench_layer_norm(torch, native, rows, n, steps, warmup, rotate=1, seed=1):
     import numpy as np
 
     rng = np.random.default_rng(seed)
-    xs = [torch.randn(rows, n, device="cuda") for _ in range(rotate)]
+    xs = [torch.from_numpy(rng.standard_normal((rows, n), dtype=np.float32)).cuda() for _ in range(rotate)]
     ys = [torch.empty_like(x) for x in xs]
     g = torch.from_numpy((1 + 0.1 * rng.standard_normal(n)).astype(np.float32)).cuda()
     b = torch.from_numpy((0.1 * rng.standard_normal(n)).astype(np.float32)).cuda()
@@ -363,6 +363,92 @@ def bench_config4(torch, steps, warmup):
     return res
 
 
+class RotatingArgs:
+    """Argument lists for successive Executes: `a`, then `b` (when given),
+    alternately."""
+
+    def __init__(self, a, b=None):
+        self.sets, self.i = [a] + ([b] if b else []), 0
+
+    def next(self):
+        s = self.sets[self.i % len(self.sets)]
+        self.i += 1
+        return s
+
+
+def time_pjrt_executes(torch, exe, bufs, steps, warmup):
+    """Seconds per Execute of `exe` on device-resident argument lists
+    (`bufs.next()`): a PREWARM_S pre-warm, `warmup` calls, then the host
+    clock around `steps` back-to-back Executes (enqueued on the plugin's
+    stream without waiting) and the last one's completion event.  Also
+    returns the host's own time per enqueue."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < PREWARM_S:
+        for _ in range(9):
+            exe.execute(bufs.next(), wait=False)
+        exe.execute(bufs.next(), wait=True)
+    for i in range(warmup):
+        exe.execute(bufs.next(), wait=(i == warmup - 1))
+    t0 = time.perf_counter()
+    for i in range(steps - 1):
+        outs = exe.execute(bufs.next(), wait=False)
+    t_enq = time.perf_counter() - t0
+    outs = exe.execute(bufs.next(), wait=True)
+    dt = (time.perf_counter() - t0) / steps
+    return dt, outs, t_enq / max(1, steps - 1)
+
+
+def bench_sdpa_pjrt(torch, which, steps, warmup, direct_us):
+    """Configs 3 and 5 as jitted StableHLO modules through the drop-in route
+    (Client_Compile once, then LoadedExecutable_Execute on device views of
+    the inputs the C-ABI legs time), beside the direct C-ABI figure."""
+    import numpy as np
+
+    import mlir_modules
+    from jax_mlx_amd import pjrt
+
+    client = pjrt.Client()
+    if which == 3:
+        B, H, T, d = 4, 32, 2048, 128
+        rng = np.random.default_rng(3)
+        arrays = [torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32)).to("cuda").bfloat16()
+                  for _ in range(3)]
+        text = mlir_modules.sdpa_bhtd_module(B=B, H=H, T=T, D=d, dt="bf16", causal=True)
+    else:
+        B, Hq, Hkv, d, S = 16, 32, 8, 128, 8192
+        rng = np.random.default_rng(5)
+        draw = lambda shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda().bfloat16()  # noqa
+        q = draw((B, Hq, 1, d))
+        k, v = draw((B, Hkv, S, d)), draw((B, Hkv, S, d))
+        lens = rng.integers(1024, 8192, size=B, endpoint=True)
+        k2, v2 = draw((B, Hkv, S, d)), draw((B, Hkv, S, d))  # the C-ABI leg's second (rotated) K/V set
+        mask = torch.from_numpy(np.where(np.arange(S)[None] < lens[:, None], 0.0, -np.inf)
+                                .reshape(B, 1, 1, S).astype(np.float32)).cuda()
+        arrays = [q, k, v, mask, k2, v2]
+        text = mlir_modules.gqa_decode_module(B=B, S=S)
+    t0 = time.perf_counter()
+    exe = client.compile(text)
+    compile_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    views = [client.buffer_view(t) for t in arrays]
+    # Config 5 alternates two K/V sets (537 MB each) as the C-ABI leg does, so
+    # neither reads K/V from the 256 MB Infinity Cache of the previous call.
+    bufs = RotatingArgs(views[:4], None if which == 3 else [views[0], views[4], views[5], views[3]])
+    dt, outs, enq = time_pjrt_executes(torch, exe, bufs, steps, warmup)
+    steps_labels = [st["label"] for st in client.api.inspect(text)["plan"]["steps"]]
+    res = {"us_per_execute": round(dt * 1e6, 2), "direct_c_abi_us": round(direct_us, 2),
+           "ratio_to_c_abi": round(dt * 1e6 / direct_us, 4), "host_enqueue_us": round(enq * 1e6, 2),
+           "compile_s": round(compile_s, 3),
+           "plan_steps": steps_labels,
+           "timing": "host clock around back-to-back Executes on device views, last completion event"}
+    if which == 3:
+        res["TFLOPs"] = sdpa_causal_flops(4, 32, 2048, 128) / dt / 1e12
+    del outs, bufs, views
+    exe.destroy()
+    client.destroy()
+    return res
+
+
 def bench_config4_gemms(torch, native, steps, warmup):
     """Config 4's four dense layers one at a time, as the plan runs them: the
     f32 tile GEMM with its elementwise consumer fused (mfx_gemm_ew: QKV +
@@ -478,6 +564,9 @@ ONLY = {
         "sweep": [bench_layer_norm(torch, native, 1 << 20, 512, k, w),
                   bench_layer_norm(torch, native, 65536, 4096, k, w)]},
     "copy": lambda torch, native, k, w: bench_copy(torch, k, w),
+    "pjrt": lambda torch, native, k, w: {
+        "config3_pjrt": bench_sdpa_pjrt(torch, 3, k, w, bench_config3(torch, native, k, w)["avg_ms"] * 1e3),
+        "config5_pjrt": bench_sdpa_pjrt(torch, 5, k, w, bench_config5(torch, native, k, w)["avg_us"])},
     "config3_bwd": lambda torch, native, k, w: bench_config3_bwd(torch, native, k, w),
     "ln_bwd": lambda torch, native, k, w: {
         "sweep": [bench_layer_norm_bwd(torch, native, 1 << 20, 512, k, w),
@@ -575,6 +664,11 @@ def main() -> int:
         extra["config2_sdpa_f32"] = bench_config2(torch, native, 200, 20)
         log("config 5: GQA decode bf16 + RMSNorm(q)")
         extra["config5_decode"] = bench_config5(torch, native, 50, 5)
+        torch.cuda.empty_cache()
+        log("configs 3 and 5 through PJRT (Client_Compile + Execute)")
+        extra["config3_pjrt"] = bench_sdpa_pjrt(torch, 3, 20, 3, c3["avg_ms"] * 1e3)
+        torch.cuda.empty_cache()
+        extra["config5_pjrt"] = bench_sdpa_pjrt(torch, 5, 50, 5, extra["config5_decode"]["avg_us"])
         torch.cuda.empty_cache()
         log("config 3 backward: mfx_sdpa_bwd causal bf16 [4,32,2048,128]")
         extra["config3_sdpa_bwd"] = bench_config3_bwd(torch, native, 10, 2)

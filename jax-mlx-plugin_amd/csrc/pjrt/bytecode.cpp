@@ -1,13 +1,20 @@
-// MLIR bytecode (StableHLO portable artifact) -> MLIR text.
+// Program bytes -> MLIR text.
 //
-// jaxlib hands PJRT plugins the module as a serialized portable artifact
-// ("ML\xefR" bytecode).  Deserialising it needs MLIR's StableHLO dialect,
-// which lives in the jaxlib already loaded in the calling process; like the
-// reference (src/jax_mlx_pjrt.cpp:749-822) the plugin calls into that
-// interpreter, here through jax_mlx_amd._bytecode.to_text().  The Python C-API
-// symbols are resolved with dlsym at run time so the library also loads in
-// processes without Python (the C++ / ctypes test drivers), where only MLIR
-// text is accepted.
+// jaxlib hands PJRT plugins the module as a serialized StableHLO portable
+// artifact ("ML\xefR" bytecode); other hosts (Reactant.jl, C drivers) may hand
+// MLIR text.  The plugin's parser reads text, so bytecode is turned into text
+// first, by whichever MLIR runtime the calling process already holds.  Two
+// routes are tried in the reference's order (src/jax_mlx_pjrt.cpp:671-830):
+//
+//   1. the MLIR C API exported into the process (Reactant.jl and other hosts
+//      without Python): stablehloDeserializePortableArtifactNoError, with
+//      mlirModuleCreateParse as the fallback, printed by mlirOperationPrint
+//      (reference :674-745);
+//   2. the jaxlib of a running Python interpreter, through
+//      jax_mlx_amd._bytecode.to_text() (reference :749-822).
+//
+// Every symbol is resolved with dlsym at run time, so the library loads in any
+// process; with neither runtime present, only MLIR text is accepted.
 #include <dlfcn.h>
 
 #include <cstring>
@@ -20,6 +27,85 @@ bool is_mlir_bytecode(const char* data, size_t size) {
 }
 
 namespace {
+
+// ---- route 1: the MLIR C API ----------------------------------------------
+//
+// The C API passes its handles as one-pointer structs and strings as
+// (data, length) pairs, by value; these mirror that layout.
+struct MHandle {
+  void* ptr;
+};
+struct MString {
+  const char* data;
+  size_t length;
+};
+
+struct MlirCApi {
+  MHandle (*context_create)();
+  void (*context_destroy)(MHandle);
+  void (*allow_unregistered)(MHandle, bool);
+  void (*load_all_dialects)(MHandle);
+  MHandle (*deserialize_artifact)(MString, MHandle);
+  MHandle (*module_parse)(MHandle, MString);
+  void (*module_destroy)(MHandle);
+  MHandle (*module_operation)(MHandle);
+  void (*operation_print)(MHandle, void (*)(MString, void*), void*);
+  // A usable route needs a context, a module source and a printer.
+  bool usable() const {
+    return context_create && module_operation && operation_print && (deserialize_artifact || module_parse);
+  }
+};
+
+template <class F>
+void bind(F& f, const char* name) {
+  f = reinterpret_cast<F>(dlsym(RTLD_DEFAULT, name));
+}
+
+// Resolved per call: a host may load its MLIR runtime after this library.
+MlirCApi find_mlir_capi() {
+  MlirCApi a{};
+  bind(a.context_create, "mlirContextCreate");
+  bind(a.context_destroy, "mlirContextDestroy");
+  bind(a.allow_unregistered, "mlirContextSetAllowUnregisteredDialects");
+  bind(a.load_all_dialects, "mlirContextLoadAllAvailableDialects");
+  bind(a.deserialize_artifact, "stablehloDeserializePortableArtifactNoError");
+  bind(a.module_parse, "mlirModuleCreateParse");
+  bind(a.module_destroy, "mlirModuleDestroy");
+  bind(a.module_operation, "mlirModuleGetOperation");
+  bind(a.operation_print, "mlirOperationPrint");
+  return a;
+}
+
+void append_chunk(MString s, void* user) { static_cast<std::string*>(user)->append(s.data, s.length); }
+
+// Returns true with the module's text; false with the reason otherwise.
+bool via_mlir_capi(const MlirCApi& api, const char* data, size_t size, std::string& text, std::string& err) {
+  MHandle ctx = api.context_create();
+  if (!ctx.ptr) {
+    err = "mlirContextCreate returned no context";
+    return false;
+  }
+  if (api.allow_unregistered) api.allow_unregistered(ctx, true);
+  if (api.load_all_dialects) api.load_all_dialects(ctx);
+  const MString in{data, size};
+  MHandle mod{nullptr};
+  if (api.deserialize_artifact) mod = api.deserialize_artifact(in, ctx);
+  if (!mod.ptr && api.module_parse) mod = api.module_parse(ctx, in);
+  bool ok = false;
+  if (mod.ptr) {
+    text.clear();
+    api.operation_print(api.module_operation(mod), append_chunk, &text);
+    ok = !text.empty();
+    if (!ok) err = "mlirOperationPrint produced no text";
+    if (api.module_destroy) api.module_destroy(mod);
+  } else {
+    err = "the MLIR C API could neither deserialize nor parse the module";
+  }
+  if (api.context_destroy) api.context_destroy(ctx);
+  return ok;
+}
+
+// ---- route 2: the calling process's Python and jaxlib ------------------------
 
 typedef void PyObject;
 struct PyApi {
@@ -37,11 +123,10 @@ struct PyApi {
   bool ok = false;
 };
 
-PyApi load_api() {
+PyApi load_py_api() {
   PyApi a{};
-  void* h = RTLD_DEFAULT;
-#define SYM(name)                                                  \
-  a.name = reinterpret_cast<decltype(a.name)>(dlsym(h, #name));   \
+#define SYM(name)          \
+  bind(a.name, #name);     \
   if (!a.name) return a;
   SYM(Py_IsInitialized)
   SYM(PyGILState_Ensure)
@@ -78,14 +163,7 @@ std::string py_error(const PyApi& a) {
   return msg;
 }
 
-}  // namespace
-
-bool bytecode_to_text(const char* data, size_t size, std::string& text, std::string& err) {
-  static const PyApi api = load_api();
-  if (!api.ok || !api.Py_IsInitialized()) {
-    err = "bytecode needs the jaxlib of a running Python process; pass MLIR text instead";
-    return false;
-  }
+bool via_python(const PyApi& api, const char* data, size_t size, std::string& text, std::string& err) {
   const int gil = api.PyGILState_Ensure();
   bool ok = false;
   PyObject* mod = api.PyImport_ImportModule("jax_mlx_amd._bytecode");
@@ -100,11 +178,49 @@ bool bytecode_to_text(const char* data, size_t size, std::string& text, std::str
       ok = true;
     }
   }
-  if (!ok) err = py_error(api);
+  if (!ok) err = "jax_mlx_amd._bytecode.to_text: " + py_error(api);
   for (PyObject* o : {res, bytes, fn, mod})
     if (o) api.Py_DecRef(o);
   api.PyGILState_Release(gil);
   return ok;
+}
+
+}  // namespace
+
+// MLIR text of a program: the bytes themselves when they are not bytecode,
+// otherwise the first route that converts them.  `route` names what was used
+// ("text", "mlir-capi", "python").  On failure `err` says what each route
+// reported, or that neither exists in this process.
+bool program_text(const char* data, size_t size, std::string& text, std::string& route, std::string& err) {
+  if (!is_mlir_bytecode(data, size)) {
+    text.assign(data, size);
+    route = "text";
+    return true;
+  }
+  std::string why;
+  const MlirCApi capi = find_mlir_capi();
+  if (capi.usable()) {
+    std::string e;
+    if (via_mlir_capi(capi, data, size, text, e)) {
+      route = "mlir-capi";
+      return true;
+    }
+    why = "MLIR C API: " + e;
+  }
+  if (why.empty())
+    why = "no MLIR C API (mlirContextCreate, stablehloDeserializePortableArtifactNoError, mlirOperationPrint)";
+  static const PyApi py = load_py_api();
+  if (py.ok && py.Py_IsInitialized()) {
+    std::string e;
+    if (via_python(py, data, size, text, e)) {
+      route = "python";
+      return true;
+    }
+    err = why + "; " + e;
+  } else {
+    err = why + "; no Python interpreter in this process; pass MLIR text instead";
+  }
+  return false;
 }
 
 }  // namespace mfxp

@@ -33,8 +33,7 @@
 
 namespace mfxp {
 // bytecode.cpp
-bool is_mlir_bytecode(const char* data, size_t size);
-bool bytecode_to_text(const char* data, size_t size, std::string& text, std::string& err);
+bool program_text(const char* data, size_t size, std::string& text, std::string& route, std::string& err);
 }  // namespace mfxp
 
 using namespace mfxp;
@@ -301,6 +300,7 @@ struct PJRT_Buffer {
 struct PJRT_Executable {
   std::atomic<int> refs{1};
   std::string name, fingerprint;
+  std::string text;  // the MLIR text the plan was built from (Serialize)
   std::unique_ptr<Plan> plan;
   std::vector<PJRT_Buffer_Type> out_types;
   std::vector<int64_t> out_dims;
@@ -536,9 +536,14 @@ PJRT_Error* Client_Create(PJRT_Client_Create_Args* args) {
     d->desc.debug = "MI355X:" + std::to_string(i);
     d->desc.tostr = "MI355XDevice(id=" + std::to_string(i) + ", arch=" + d->desc.arch + ")";
     d->desc.core_count = prop.multiProcessorCount;
+    // Non-blocking: launches on this stream do not order themselves after
+    // the legacy null stream (that implicit wait put a gap of several us
+    // before every launch).  Work the plugin depends on is ordered
+    // explicitly: host copies run on this stream, and a device view waits
+    // for its producer's stream (CreateViewOfDeviceBuffer).  Default priority.
     e = hipSetDevice(i);
-    if (e == hipSuccess) e = hipStreamCreate(&d->stream);
-    if (e != hipSuccess) return hip_error(e, "hipStreamCreate");
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_error(e, "hipStreamCreateWithFlags");
     auto m = std::make_unique<PJRT_Memory>();
     m->id = i;
     m->debug = "device memory of MI355X:" + std::to_string(i);
@@ -647,6 +652,8 @@ PJRT_Error* Client_AddressableMemories(PJRT_Client_AddressableMemories_Args* arg
   return nullptr;
 }
 
+PJRT_Error* load_text(PJRT_Client* client, const std::string& text, PJRT_LoadedExecutable** out);
+
 PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
   CHECK_ARGS(PJRT_Client_Compile_Args, executable);
   GUARD_BEGIN
@@ -655,14 +662,15 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
   std::string format(prog->format ? prog->format : "", prog->format ? prog->format_size : 0);
   if (format != "mlir")
     return make_error(PJRT_Error_Code_INVALID_ARGUMENT, "Compile: program format '" + format + "' (expected 'mlir')");
-  std::string text;
-  if (is_mlir_bytecode(prog->code, prog->code_size)) {
-    std::string err;
-    if (!bytecode_to_text(prog->code, prog->code_size, text, err))
-      return make_error(PJRT_Error_Code_UNIMPLEMENTED, "Compile: MLIR bytecode: " + err);
-  } else {
-    text.assign(prog->code, prog->code_size);
-  }
+  std::string text, route, err;
+  if (!program_text(prog->code, prog->code_size, text, route, err))
+    return make_error(PJRT_Error_Code_UNIMPLEMENTED, "Compile: MLIR bytecode: " + err);
+  return load_text(args->client, text, &args->executable);
+  GUARD_END
+}
+
+// Plans `text` for `client` (Client_Compile and DeserializeAndLoad).
+PJRT_Error* load_text(PJRT_Client* client, const std::string& text, PJRT_LoadedExecutable** out) {
   Compiled c;
   try {
     c = compile_text(text);
@@ -671,6 +679,7 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
   }
   auto* exe = new PJRT_Executable();
   exe->name = c.module_name.empty() ? "main" : c.module_name;
+  exe->text = text;
   exe->fingerprint = fnv1a_hex(text);
   exe->json = to_json(*c.main, &c.stats);
   exe->plan = std::move(c.plan);
@@ -693,10 +702,9 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
   exe->cost.push_back(nv);
   auto* le = new PJRT_LoadedExecutable();
   le->exe = exe;
-  le->client = args->client;
-  args->executable = le;
+  le->client = client;
+  *out = le;
   return nullptr;
-  GUARD_END
 }
 
 PJRT_Error* Client_DefaultDeviceAssignment(PJRT_Client_DefaultDeviceAssignment_Args* args) {
@@ -805,9 +813,22 @@ PJRT_Error* Client_CreateViewOfDeviceBuffer(PJRT_Client_CreateViewOfDeviceBuffer
   t.dims.assign(args->dims, args->dims + args->num_dims);
   if (args->layout && args->layout->type != PJRT_Buffer_MemoryLayout_Type_Tiled)
     return make_error(PJRT_Error_Code_UNIMPLEMENTED, "CreateViewOfDeviceBuffer: strided layouts");
+  PJRT_Device* dev = pick_device(args->client, args->device, nullptr);
+  // The memory is ready once the work enqueued so far on the producer's
+  // stream (`stream`, or the legacy null stream when none is given) is done:
+  // the plugin's stream waits for it there before anything reads the view.
+  {
+    hipError_t e = hipSetDevice(dev->ordinal);
+    hipEvent_t ev = nullptr;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(ev, reinterpret_cast<hipStream_t>(args->stream));
+    if (e == hipSuccess) e = hipStreamWaitEvent(dev->stream, ev, 0);
+    if (ev) (void)hipEventDestroy(ev);
+    if (e != hipSuccess) return hip_error(e, "CreateViewOfDeviceBuffer: ordering after the producer's stream");
+  }
   auto* b = new PJRT_Buffer();
   b->client = args->client;
-  b->device = pick_device(args->client, args->device, nullptr);
+  b->device = dev;
   b->ptr = args->device_buffer_ptr;
   b->bytes = (size_t)t.bytes();
   b->type = t;
@@ -1032,11 +1053,55 @@ PJRT_Error* Executable_OutputMemoryKinds(PJRT_Executable_OutputMemoryKinds_Args*
 PJRT_Error* Executable_OptimizedProgram(PJRT_Executable_OptimizedProgram_Args* args) {
   return unimplemented("PJRT_Executable_OptimizedProgram");
 }
+// Serialized executable: the magic kSerialMagic, a format version, the text
+// length (little-endian u32, u64) and the module text.  The plan is rebuilt
+// from the text on load (same parser, rewriter and planner, so the same
+// launches), which makes the blob independent of device addresses and of the
+// hipRTC code objects cached per process.  (The reference returns an empty
+// blob, src/jax_mlx_pjrt.cpp:1585-1601.)
+constexpr char kSerialMagic[8] = {'M', 'F', 'X', 'P', 'J', 'R', 'T', '\n'};
+constexpr uint32_t kSerialVersion = 1;
+constexpr size_t kSerialHeader = sizeof kSerialMagic + 4 + 8;
+
+void delete_serialized(PJRT_SerializedExecutable* p) { delete reinterpret_cast<std::string*>(p); }
+
 PJRT_Error* Executable_Serialize(PJRT_Executable_Serialize_Args* args) {
-  return unimplemented("PJRT_Executable_Serialize");
+  CHECK_ARGS(PJRT_Executable_Serialize_Args, serialized_executable_deleter);
+  if (!args->executable) return make_error(PJRT_Error_Code_INVALID_ARGUMENT, "Serialize: no executable");
+  const std::string& text = args->executable->text;
+  auto* blob = new std::string(kSerialMagic, sizeof kSerialMagic);
+  const uint64_t n = text.size();
+  for (int i = 0; i < 4; ++i) blob->push_back((char)((kSerialVersion >> (8 * i)) & 0xff));
+  for (int i = 0; i < 8; ++i) blob->push_back((char)((n >> (8 * i)) & 0xff));
+  blob->append(text);
+  args->serialized_bytes = blob->data();
+  args->serialized_bytes_size = blob->size();
+  args->serialized_executable = reinterpret_cast<PJRT_SerializedExecutable*>(blob);
+  args->serialized_executable_deleter = delete_serialized;
+  return nullptr;
 }
+
 PJRT_Error* Executable_DeserializeAndLoad(PJRT_Executable_DeserializeAndLoad_Args* args) {
-  return unimplemented("PJRT_Executable_DeserializeAndLoad");
+  CHECK_ARGS(PJRT_Executable_DeserializeAndLoad_Args, loaded_executable);
+  GUARD_BEGIN
+  if (!args->client) return make_error(PJRT_Error_Code_INVALID_ARGUMENT, "DeserializeAndLoad: no client");
+  const char* b = args->serialized_executable;
+  const size_t size = b ? args->serialized_executable_size : 0;
+  if (size < kSerialHeader || std::memcmp(b, kSerialMagic, sizeof kSerialMagic) != 0)
+    return make_error(PJRT_Error_Code_INVALID_ARGUMENT,
+                      "DeserializeAndLoad: not an executable serialized by this plugin");
+  uint32_t version = 0;
+  uint64_t n = 0;
+  for (int i = 0; i < 4; ++i) version |= (uint32_t)(unsigned char)b[sizeof kSerialMagic + i] << (8 * i);
+  for (int i = 0; i < 8; ++i) n |= (uint64_t)(unsigned char)b[sizeof kSerialMagic + 4 + i] << (8 * i);
+  if (version != kSerialVersion)
+    return make_error(PJRT_Error_Code_INVALID_ARGUMENT,
+                      "DeserializeAndLoad: serialized format version " + std::to_string(version) +
+                          ", this plugin reads version " + std::to_string(kSerialVersion));
+  if (n != size - kSerialHeader)
+    return make_error(PJRT_Error_Code_INVALID_ARGUMENT, "DeserializeAndLoad: truncated or padded executable");
+  return load_text(args->client, std::string(b + kSerialHeader, (size_t)n), &args->loaded_executable);
+  GUARD_END
 }
 PJRT_Error* Executable_OutputElementTypes(PJRT_Executable_OutputElementTypes_Args* args) {
   CHECK_ARGS(PJRT_Executable_OutputElementTypes_Args, num_output_types);
@@ -1617,8 +1682,11 @@ MFXP_EXPORT const PJRT_Api* GetPjrtApi(void) {
 MFXP_EXPORT int mfx_pjrt_inspect(const char* text, size_t size, char** json_out) {
   if (!json_out) return PJRT_Error_Code_INVALID_ARGUMENT;
   try {
-    Compiled c = compile_text(std::string(text ? text : "", text ? size : 0));
-    *json_out = dup_cstr("{\"graph\": " + to_json(*c.main, &c.stats) + ", \"plan\": " + c.plan->summary_json() + "}");
+    std::string src, route, err;
+    if (!program_text(text ? text : "", text ? size : 0, src, route, err)) throw std::runtime_error(err);
+    Compiled c = compile_text(src);
+    *json_out = dup_cstr("{\"source\": \"" + route + "\", \"graph\": " + to_json(*c.main, &c.stats) +
+                         ", \"plan\": " + c.plan->summary_json() + "}");
     return 0;
   } catch (const std::exception& e) {
     std::string m = e.what();

@@ -97,6 +97,14 @@ CreateViewArgs = _args("CreateViewArgs", [
     ("client", c_void_p), ("device_buffer_ptr", c_void_p), ("dims", POINTER(c_int64)), ("num_dims", c_size_t),
     ("element_type", c_int), ("layout", c_void_p), ("device", c_void_p), ("on_delete_callback", c_void_p),
     ("on_delete_callback_arg", c_void_p), ("stream", ctypes.c_ssize_t), ("buffer", c_void_p), ("memory", c_void_p)])
+SerializeArgs = _args("SerializeArgs", [("executable", c_void_p), ("serialized_bytes", c_void_p),
+                                        ("serialized_bytes_size", c_size_t), ("serialized_executable", c_void_p),
+                                        ("serialized_executable_deleter", ctypes.CFUNCTYPE(None, c_void_p))])
+DeserializeArgs = _args("DeserializeArgs", [("client", c_void_p), ("serialized_executable", c_void_p),
+                                            ("serialized_executable_size", c_size_t),
+                                            ("loaded_executable", c_void_p),
+                                            ("overridden_serialized_compile_options", c_char_p),
+                                            ("overridden_serialized_compile_options_size", c_size_t)])
 ExecuteOptions = _args("ExecuteOptions", [
     ("send_callbacks", c_void_p), ("recv_callbacks", c_void_p), ("num_send_ops", c_size_t),
     ("num_recv_ops", c_size_t), ("launch_id", c_int), ("non_donatable_input_indices", c_void_p),
@@ -189,12 +197,14 @@ class Api:
             code, msg = self.error_info(err)
             raise PjrtError(code, msg)
 
-    def inspect(self, text: str) -> dict:
-        """Parse + rewrite + plan without a device (mfx_pjrt_inspect)."""
+    def inspect(self, text) -> dict:
+        """Parse + rewrite + plan without a device (mfx_pjrt_inspect).  `text`
+        is MLIR text (str) or program bytes (MLIR text, or bytecode that the
+        process's MLIR runtime converts, as Client_Compile does)."""
         import json
 
         out = c_void_p()
-        b = text.encode()
+        b = text.encode() if isinstance(text, str) else bytes(text)
         rc = self.lib.mfx_pjrt_inspect(b, len(b), ctypes.byref(out))
         s = ctypes.string_at(out.value).decode()
         self.lib.mfx_pjrt_free(out)
@@ -341,6 +351,15 @@ class Executable:
             self.client.api.call("Event_Destroy", new(EventArgs, event=events[0]))
         return [Buffer(self.client, out_arr[i]) for i in range(n_out)]
 
+    def serialize(self) -> bytes:
+        """Executable_Serialize: the plugin's serialized form (its bytes are
+        copied out and the plugin's copy freed with its deleter)."""
+        a = new(SerializeArgs, executable=self.exe)
+        self.client.api.call("Executable_Serialize", a)
+        data = ctypes.string_at(a.serialized_bytes, a.serialized_bytes_size)
+        a.serialized_executable_deleter(a.serialized_executable)
+        return data
+
     def destroy(self):
         if self.handle:
             self.client.api.call("Executable_Destroy", new(LoadedExecArgs, executable=self.exe))
@@ -383,6 +402,14 @@ class Client:
                 compile_options_size=0)
         self.api.call("Client_Compile", a)
         return Executable(self, a.executable)
+
+    def deserialize(self, blob: bytes) -> Executable:
+        """Executable_DeserializeAndLoad of Executable.serialize()'s bytes."""
+        buf = ctypes.create_string_buffer(blob, len(blob))
+        a = new(DeserializeArgs, client=self.handle, serialized_executable=ctypes.cast(buf, c_void_p),
+                serialized_executable_size=len(blob))
+        self.api.call("Executable_DeserializeAndLoad", a)
+        return Executable(self, a.loaded_executable)
 
     def buffer_from_host(self, tensor, byte_strides=None) -> Buffer:
         """BufferFromHostBuffer from a host torch tensor (or numpy array)."""

@@ -335,12 +335,7 @@ def test_sdpa_bf16_golden(cuda, nat, golden):
     check_sdpa(out, golden["sdpa_bf16_out_causal"], "bf16")
 
 
-# (batch, head) pairs of config 3 checked against the oracle at full size.
-# The prefill kernels deal (batch*Hq + head) = bh to XCD bh % 8, slot
-# (bh / 8) % 4 of a four-head group, group bh / 32: these eight cover every
-# XCD residue, every group slot twice and every group twice.
-CONFIG3_BH = [0, 9, 50, 59, 68, 77, 118, 127]
-CONFIG3_HEADS = [(bh // 32, bh % 32) for bh in CONFIG3_BH]
+from config3_heads import CONFIG3_BH, CONFIG3_HEADS
 
 
 def test_config3_heads_cover_every_xcd_and_slot():

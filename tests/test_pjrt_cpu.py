@@ -9,6 +9,7 @@ tests of these fusions (its tests/ hold test_compilation_coverage.py,
 test_complex.py, test_exhaustive.py and test_exhaustive_while.py, none of
 which covers SDPA, LayerNorm or RMSNorm), so the module texts are this
 repository's own (tests/mlir_modules.py)."""
+import json
 import math
 import re
 import subprocess
@@ -112,6 +113,119 @@ def test_c_host_binding(tmp_path):
 
     if not torch.cuda.is_available():
         assert int(code) == 9  # FAILED_PRECONDITION
+
+
+INSPECT_HOST = r"""
+#include <dlfcn.h>
+#include <stdio.h>
+#include <stdlib.h>
+/* argv: plugin library, MLIR C-API library to load RTLD_GLOBAL first (or -),
+ * file holding the program bytes */
+int main(int argc, char** argv) {
+  void* capi = NULL;
+  if (argc != 4) return 2;
+  if (argv[2][0] != '-' && !(capi = dlopen(argv[2], RTLD_NOW | RTLD_GLOBAL))) return 3;
+  void* h = dlopen(argv[1], RTLD_NOW | RTLD_LOCAL);
+  if (!h) return 4;
+  int (*inspect)(const char*, size_t, char**) = (int (*)(const char*, size_t, char**))dlsym(h, "mfx_pjrt_inspect");
+  void (*release)(char*) = (void (*)(char*))dlsym(h, "mfx_pjrt_free");
+  FILE* f = fopen(argv[3], "rb");
+  if (!f) return 5;
+  fseek(f, 0, SEEK_END);
+  long n = ftell(f);
+  fseek(f, 0, SEEK_SET);
+  char* buf = malloc(n ? n : 1);
+  if (fread(buf, 1, n, f) != (size_t)n) return 6;
+  fclose(f);
+  char* json = NULL;
+  int rc = inspect(buf, (size_t)n, &json);
+  printf("%d\n%s\n", rc, json);
+  release(json);
+  if (capi) {
+    int (*live)(void) = (int (*)(void))dlsym(capi, "mlir_stub_live");
+    int (*calls)(void) = (int (*)(void))dlsym(capi, "mlir_stub_calls");
+    printf("%d %d\n", live(), calls());
+  }
+  free(buf);
+  return 0;
+}
+"""
+
+
+@pytest.fixture(scope="module")
+def inspect_host(tmp_path_factory):
+    """A C process without Python that inspects a program file through the
+    plugin, optionally with the MLIR C-API test double loaded first."""
+    d = tmp_path_factory.mktemp("capi")
+    (d / "host.c").write_text(INSPECT_HOST)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", str(d / "host.c"), "-o", str(d / "host"), "-ldl"],
+                   check=True)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-shared", "-fPIC",
+                    str(REPO / "tests" / "capi" / "mlir_capi_stub.c"), "-o", str(d / "libmlir_capi_stub.so")],
+                   check=True)
+
+    def run(program: bytes, with_capi: bool):
+        f = d / "program.bin"
+        f.write_bytes(program)
+        stub = str(d / "libmlir_capi_stub.so") if with_capi else "-"
+        out = subprocess.run([str(d / "host"), str(pjrt.PLUGIN_LIB), stub, str(f)], capture_output=True,
+                             text=True, timeout=60)
+        assert out.returncode == 0, (out.returncode, out.stderr)
+        lines = out.stdout.splitlines()
+        doc = json.loads(lines[1])
+        counts = tuple(int(x) for x in lines[2].split()) if with_capi else None
+        return int(lines[0]), doc, counts
+
+    return run
+
+
+BYTECODE = b"ML\xefR"
+
+
+@pytest.mark.parametrize("tag", [b"VHLO:", b"PARSE:"])
+def test_bytecode_through_mlir_capi(inspect_host, tag):
+    """Route 1 (reference src/jax_mlx_pjrt.cpp:674-745): with the MLIR C API
+    in the process, bytecode is deserialised (or, failing that, parsed) and
+    printed through it, and the module fuses as its text does.  Every
+    context and module the plugin creates is destroyed."""
+    text = M.layer_norm_module().encode()
+    rc, doc, (live, calls) = inspect_host(BYTECODE + tag + text, True)
+    assert rc == 0, doc
+    assert doc["source"] == "mlir-capi"
+    assert [n["op"] for n in fused(doc)] == [n["op"] for n in fused(inspect_text(text))]
+    assert live == 0 and calls == 2
+
+
+def inspect_text(text: bytes):
+    return pjrt.Api().inspect(text)
+
+
+def test_bytecode_mlir_capi_failure_names_both_routes(inspect_host):
+    rc, doc, (live, _) = inspect_host(BYTECODE + b"not an artifact", True)
+    assert rc == 3 and live == 0
+    assert "MLIR C API could neither deserialize nor parse" in doc["error"]
+    assert "no Python interpreter" in doc["error"] and "pass MLIR text" in doc["error"]
+
+
+def test_bytecode_without_any_mlir_runtime(inspect_host):
+    """Route 3: a host with neither the MLIR C API nor Python gets an error
+    asking for MLIR text; text itself is accepted there."""
+    rc, doc, _ = inspect_host(BYTECODE + b"VHLO:" + M.layer_norm_module().encode(), False)
+    assert rc == 3
+    assert "no MLIR C API" in doc["error"] and "pass MLIR text instead" in doc["error"]
+    rc, doc, _ = inspect_host(M.layer_norm_module().encode(), False)
+    assert rc == 0 and doc["source"] == "text"
+
+
+def test_bytecode_through_python_without_jax(api):
+    """Route 2 (reference :749-822) in this Python process, which has no jax:
+    the call returns an error naming the missing module (no crash), after
+    reporting that no MLIR C API is loaded."""
+    with pytest.raises(pjrt.PjrtError) as e:
+        api.inspect(BYTECODE + b"VHLO:" + M.layer_norm_module().encode())
+    assert e.value.code_name == "INVALID_ARGUMENT"
+    assert "no MLIR C API" in e.value.message
+    assert "jax_mlx_amd._bytecode.to_text" in e.value.message and "jax" in e.value.message.split("to_text:")[1]
 
 
 def test_jax_modules_import_without_jax():

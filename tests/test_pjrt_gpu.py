@@ -9,6 +9,8 @@ generic ops (rocBLAS GEMMs, the elementwise interpreter, reductions) carry the
 f32 tolerance stated at each test."""
 import math
 
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -173,6 +175,52 @@ def test_sdpa_causal_bhtd_bf16(client, oracle):
     q, k, v = (bf16_round(rng.standard_normal((1, 4, 256, 128))) for _ in range(3))
     (o,) = run(client, M.sdpa_bhtd_module(B=1, H=4, T=256, D=128, dt="bf16", causal=True), [q, k, v], ["bf16"] * 3)
     assert rel_inf(o, oracle.sdpa(q, k, v, 1 / math.sqrt(128), causal=True)) <= BF16_REL_TOL
+
+
+def _device_bf16(cuda, a):
+    return cuda.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda().bfloat16()
+
+
+def test_sdpa_config3_full_size_through_pjrt(client, oracle, cuda):
+    """Config 3 as a jitted module through Client_Compile / Execute at full
+    size ([4, 32, 2048, 128] bf16, causal): bit-identical to the direct C-ABI
+    call on the same inputs (same kernel and arguments), eight heads (one per
+    XCD residue and group slot) against the fp64 oracle, row 0 = v0."""
+    from config3_heads import CONFIG3_HEADS
+    from jax_mlx_amd import native
+
+    rng = np.random.default_rng(3)
+    shape = (4, 32, 2048, 128)
+    q, k, v = (bf16_round(rng.standard_normal(shape).astype(np.float32)) for _ in range(3))
+    (o,) = run(client, M.sdpa_bhtd_module(B=4, H=32, T=2048, D=128, dt="bf16", causal=True), [q, k, v],
+               ["bf16"] * 3)
+    direct = native.sdpa(*(_device_bf16(cuda, a) for a in (q, k, v)), scale=128 ** -0.5, causal=True)
+    assert np.array_equal(o, direct.float().cpu().numpy().astype(np.float64))
+    assert np.array_equal(o[:, :, 0], v[:, :, 0])
+    for b, h in CONFIG3_HEADS:
+        ref = oracle.sdpa(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], 128 ** -0.5, causal=True)
+        assert rel_inf(o[b:b + 1, h:h + 1], ref) <= BF16_REL_TOL, (b, h)
+
+
+def test_gqa_decode_config5_full_size_through_pjrt(client, oracle, cuda):
+    """Config 5 through PJRT at full size: RMSNorm(q) folded into the GQA
+    decode over [16, 8, 8192, 128] K/V with a length mask from
+    default_rng(5).  Bit-identical to the direct C-ABI call; every row
+    against the fp64 oracle."""
+    from jax_mlx_amd import native
+
+    rng = np.random.default_rng(5)
+    q = bf16_round(rng.standard_normal((16, 32, 1, 128)).astype(np.float32))
+    k = bf16_round(rng.standard_normal((16, 8, 8192, 128)).astype(np.float32))
+    v = bf16_round(rng.standard_normal((16, 8, 8192, 128)).astype(np.float32))
+    lens = rng.integers(1024, 8192, size=16, endpoint=True)
+    mask = np.where(np.arange(8192)[None] < lens[:, None], 0.0, -np.inf).reshape(16, 1, 1, 8192).astype(np.float32)
+    (o,) = run(client, M.gqa_decode_module(B=16, S=8192), [q, k, v, mask], ["bf16"] * 3 + ["f32"])
+    md = cuda.from_numpy(mask).cuda()
+    direct = native.sdpa(*(_device_bf16(cuda, a) for a in (q, k, v)), scale=128 ** -0.5, mask=md, q_rms_eps=1e-6)
+    assert np.array_equal(o, direct.float().cpu().numpy().astype(np.float64))
+    qn = bf16_round(oracle.rms_norm(q, None, 1e-6).astype(np.float32))
+    assert rel_inf(o, oracle.sdpa(qn, k, v, 128 ** -0.5, mask=mask)) <= BF16_REL_TOL
 
 
 def test_dot_product_attention_btnh_causal(client, oracle):
@@ -543,6 +591,131 @@ def test_sdpa_vjp_two_cotangents(client, dt):
         assert np.array_equal(both[0], plain[0])
         for a, b in zip(got, plain[1:]):
             assert np.array_equal(a, b)
+
+
+def test_executable_serialize_round_trip(client):
+    """Executable_Serialize / DeserializeAndLoad (reference
+    src/jax_mlx_pjrt.cpp:1585-1601 stubs them): the blob holds the module
+    text; the loaded copy runs the same plan, so its outputs are bit-identical
+    to the original's.  Blobs this plugin did not write, of another format
+    version, or cut short are rejected with INVALID_ARGUMENT."""
+    from jax_mlx_amd import pjrt
+
+    rng = np.random.default_rng(44)
+    text = M.sdpa_bhtd_module(B=2, H=4, T=96, D=64, causal=True)
+    exe = client.compile(text)
+    blob = exe.serialize()
+    assert blob[:8] == b"MFXPJRT\n" and text.encode() in blob
+    again = client.deserialize(blob)
+    assert again.num_outputs == exe.num_outputs
+    qkv = [rng.standard_normal((2, 4, 96, 64)).astype(np.float32) for _ in range(3)]
+    outs = []
+    for e in (exe, again):
+        bufs = [client.buffer_from_host(host_arg(a, "f32")) for a in qkv]
+        o = e.execute(bufs)
+        outs.append([t.to_torch().numpy() for t in o])
+        for t in o + bufs:
+            t.destroy()
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    assert again.serialize() == blob
+    for bad in (b"not an executable", blob[:8] + b"\x02\x00\x00\x00" + blob[12:], blob[:-1], blob + b" "):
+        with pytest.raises(pjrt.PjrtError) as err:
+            client.deserialize(bad)
+        assert err.value.code_name == "INVALID_ARGUMENT", err.value.message
+    exe.destroy()
+    again.destroy()
+
+
+COMPILE_HOST = r"""
+#include <dlfcn.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include "pjrt_mi355x.h"
+/* argv: plugin, MLIR C-API library (loaded RTLD_GLOBAL first), program file.
+ * Prints the error code of Client_Compile, then of the serialize / load
+ * round trip, then the stub's live-object count. */
+static int code_of(const PJRT_Api* api, PJRT_Error* err) {
+  if (!err) return 0;
+  PJRT_Error_GetCode_Args g = {sizeof g, NULL, err, 0};
+  api->PJRT_Error_GetCode(&g);
+  PJRT_Error_Message_Args m = {sizeof m, NULL, err, NULL, 0};
+  api->PJRT_Error_Message(&m);
+  fprintf(stderr, "%.*s\n", (int)m.message_size, m.message);
+  PJRT_Error_Destroy_Args d = {sizeof d, NULL, err};
+  api->PJRT_Error_Destroy(&d);
+  return g.code;
+}
+int main(int argc, char** argv) {
+  if (argc != 4) return 2;
+  void* capi = dlopen(argv[2], RTLD_NOW | RTLD_GLOBAL);
+  void* h = dlopen(argv[1], RTLD_NOW | RTLD_LOCAL);
+  if (!capi || !h) return 3;
+  const PJRT_Api* api = ((const PJRT_Api* (*)(void))dlsym(h, "GetPjrtApi"))();
+  FILE* f = fopen(argv[3], "rb");
+  if (!f) return 4;
+  fseek(f, 0, SEEK_END);
+  long n = ftell(f);
+  fseek(f, 0, SEEK_SET);
+  char* code = malloc(n);
+  if (fread(code, 1, n, f) != (size_t)n) return 5;
+  fclose(f);
+  PJRT_Client_Create_Args cc = {sizeof cc};
+  if (code_of(api, api->PJRT_Client_Create(&cc))) return 6;
+  PJRT_Program prog = {sizeof prog, NULL, code, (size_t)n, "mlir", 4};
+  PJRT_Client_Compile_Args ca = {sizeof ca, NULL, cc.client, &prog, "", 0, NULL};
+  int rc = code_of(api, api->PJRT_Client_Compile(&ca));
+  int rc2 = -1;
+  if (!rc) {
+    PJRT_LoadedExecutable_GetExecutable_Args g = {sizeof g, NULL, ca.executable, NULL};
+    api->PJRT_LoadedExecutable_GetExecutable(&g);
+    PJRT_Executable_Serialize_Args s = {sizeof s, NULL, g.executable};
+    rc2 = code_of(api, api->PJRT_Executable_Serialize(&s));
+    if (!rc2) {
+      PJRT_Executable_DeserializeAndLoad_Args d = {sizeof d, NULL, cc.client, s.serialized_bytes,
+                                                   s.serialized_bytes_size};
+      rc2 = code_of(api, api->PJRT_Executable_DeserializeAndLoad(&d));
+      s.serialized_executable_deleter(s.serialized_executable);
+      if (!rc2) {
+        PJRT_LoadedExecutable_Destroy_Args x = {sizeof x, NULL, d.loaded_executable};
+        api->PJRT_LoadedExecutable_Destroy(&x);
+      }
+    }
+    PJRT_Executable_Destroy_Args e = {sizeof e, NULL, g.executable};
+    api->PJRT_Executable_Destroy(&e);
+    PJRT_LoadedExecutable_Destroy_Args x = {sizeof x, NULL, ca.executable};
+    api->PJRT_LoadedExecutable_Destroy(&x);
+  }
+  PJRT_Client_Destroy_Args cd = {sizeof cd, NULL, cc.client};
+  api->PJRT_Client_Destroy(&cd);
+  printf("%d %d %d\n", rc, rc2, ((int (*)(void))dlsym(capi, "mlir_stub_live"))());
+  free(code);
+  return 0;
+}
+"""
+
+
+def test_client_compile_bytecode_via_mlir_capi_in_c_host(tmp_path):
+    """A C host without Python holding an MLIR C API (the test double in
+    tests/capi/) compiles portable-artifact bytes with Client_Compile, then
+    serializes and reloads the executable."""
+    import subprocess
+
+    from jax_mlx_amd import pjrt
+
+    repo = Path(__file__).resolve().parents[1]
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{repo / 'include'}", "-x", "c", "-",
+                    "-o", str(tmp_path / "host"), "-ldl"], input=COMPILE_HOST, text=True, check=True)
+    subprocess.run(["gcc", "-std=c11", "-shared", "-fPIC", str(repo / "tests" / "capi" / "mlir_capi_stub.c"),
+                    "-o", str(tmp_path / "libstub.so")], check=True)
+    prog = tmp_path / "prog.bin"
+    for tag, want in ((b"VHLO:", "0 0 0"), (b"PARSE:", "0 0 0"), (b"junk", "12 -1 0")):
+        prog.write_bytes(b"ML\xefR" + tag + M.layer_norm_module().encode())
+        out = subprocess.run([str(tmp_path / "host"), str(pjrt.PLUGIN_LIB), str(tmp_path / "libstub.so"),
+                              str(prog)], capture_output=True, text=True, timeout=120)
+        assert out.returncode == 0, (out.returncode, out.stderr)
+        assert out.stdout.split("\n")[0] == want, (tag, out.stdout, out.stderr)
 
 
 def test_escaping_intermediates_layer_norm(client, oracle):
