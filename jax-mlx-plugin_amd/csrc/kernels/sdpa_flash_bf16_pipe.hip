@@ -34,11 +34,83 @@
 // spill-free.  No spill is allowed here: the inline-asm LDS reads complete
 // after the asm statement, and a spill or copy of a destination register
 // placed before its lgkmcnt wait would save the value before it arrives.
+//
+// Built with -DMFX_PHASE_TIMERS (build.py --phase-timers, a separate
+// diagnostic library), every wavefront also records where its time goes:
+// s_memrealtime stamps (100 MHz) at its start, when its first tiles have
+// landed, at its loop entry and at its end, and s_memtime (shader clock)
+// sums over its phases -- S MFMAs with the exp2 of the previous tile (A), the
+// row-sum check (C), PV MFMAs (B), the barrier with the next tiles' DMA issue
+// (S) and the last tile -- read at points where none of its inline-asm LDS
+// reads is outstanding.  mfx_phase_timers_read() copies the records out;
+// jax-mlx-plugin_amd/phase_budget.py turns them into the per-tile budget.
 #include <type_traits>
 
 #include "sdpa_tiles.h"
 
+#if defined(MFX_PHASE_TIMERS)
+#define PHASE(...) __VA_ARGS__
+#else
+#define PHASE(...)
+#endif
+
 namespace mfx {
+
+#if defined(MFX_PHASE_TIMERS)
+// One record of kPhaseFields u64 per wavefront (blockIdx.x * 4 + wave).
+constexpr int kPhaseRecords = 1 << 15;
+constexpr int kPhaseFields = 20;
+__device__ unsigned long long g_phase_records[kPhaseRecords * kPhaseFields];
+
+struct PhaseClock {
+  // 32-bit fields keep the kernel's SGPR budget: cycle sums of one
+  // wavefront stay far below 2^32, and realtime stamps keep their low word
+  // (the host rebuilds them from the 64-bit end stamp).
+  unsigned rt_start, rt_ready = 0, rt_loop = 0, c_start, c_loop = 0;
+  unsigned cyc_a = 0, cyc_check = 0, cyc_b = 0, cyc_sync = 0, cyc_last = 0;
+  unsigned tiles = 0, rebases = 0, cyc_vmwait = 0, cyc_barrier = 0, cyc_dma_k = 0;
+  __device__ static unsigned now() { return (unsigned)__builtin_amdgcn_s_memtime(); }
+  __device__ static unsigned real() { return (unsigned)__builtin_amdgcn_s_memrealtime(); }
+  __device__ PhaseClock() : rt_start(real()), c_start(now()) {}
+  // Fields: 0 ids (XCC id, HW_ID, (batch*H + head), q-block), 1-3 realtime
+  // start / first tiles landed / loop entry (low words), 4 realtime end
+  // (64 bits), 5-9 cycles of phases A / check / B / barrier+DMA / last tile,
+  // 10 tiles in the loop, 11 rebases, 12 total cycles, 13 cycles before the
+  // loop, 14 (workgroup tiles, wavefront tiles), 15 cycles of the epilogue,
+  // 16 / 17 cycles of the barrier phase spent in its vmcnt wait / s_barrier,
+  // 18 cycles of issuing the K tile's DMA (the rest of the phase issues V's).
+  __device__ void write(int lane, int rec, int bh, int mblk, int N, int nw, unsigned c_epi) const {
+    unsigned xcc, hwid;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+    const unsigned c_end = now();
+    const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
+    if (lane != 0 || rec >= kPhaseRecords) return;
+    unsigned long long* r = g_phase_records + (size_t)rec * kPhaseFields;
+    r[0] = (unsigned long long)(xcc & 0xff) | ((unsigned long long)hwid << 8) | ((unsigned long long)bh << 40) |
+           ((unsigned long long)(mblk & 0xff) << 56);
+    r[1] = rt_start;
+    r[2] = rt_ready;
+    r[3] = rt_loop;
+    r[4] = rt_end;
+    r[5] = cyc_a;
+    r[6] = cyc_check;
+    r[7] = cyc_b;
+    r[8] = cyc_sync;
+    r[9] = cyc_last;
+    r[10] = tiles;
+    r[11] = rebases;
+    r[12] = c_end - c_start;
+    r[13] = c_loop - c_start;
+    r[14] = ((unsigned long long)(unsigned)N << 32) | (unsigned)nw;
+    r[15] = c_end - c_epi;
+    r[16] = cyc_vmwait;
+    r[17] = cyc_barrier;
+    r[18] = cyc_dma_k;
+  }
+};
+#endif
+
 namespace {
 
 constexpr int kBM = 128;  // query rows per workgroup
@@ -117,6 +189,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   static_assert(MS % 8 == 0 || 8 % MS == 0, "interleave");
   __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 K1 V0 V1
 
+  PHASE(PhaseClock ph;)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -327,6 +400,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       ds_tr<VB + ks * 16 * D * 2>(vr[j][1], va[dt][1]);
     };
     float ls = 0.f;
+    PHASE(const unsigned c0 = PhaseClock::now(); fence();)
     static_for<0, kPfK>(rdk);
     fence();
     static_for<0, MS>([&](auto j_tag) {
@@ -341,11 +415,16 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       for (int g = 8 + j * 8 / MS; g < 8 + (j + 1) * 8 / MS; ++g) exp_pair(sc, g, pb, ls);
       fence();
     });
+    PHASE(const unsigned c1 = PhaseClock::now(); fence();)
     if (t + 1 < nw && edge(t + 1)) mask_tile(sn, t + 1);
     float lt = lf + ls;
-    if (__builtin_amdgcn_ballot_w64(!(lt <= kSumCap))) lt = rebase(sc, pc);
+    if (__builtin_amdgcn_ballot_w64(!(lt <= kSumCap))) {
+      lt = rebase(sc, pc);
+      PHASE(++ph.rebases;)
+    }
     l_run += lt;
     lf = 0.f;
+    PHASE(fence(); const unsigned c2 = PhaseClock::now(); fence();)
     static_for<0, kPfV>(rdv);
     fence();
     static_for<0, MP>([&](auto j_tag) {
@@ -361,6 +440,8 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       for (int g = j * 8 / MP; g < (j + 1) * 8 / MP; ++g) exp_pair(sn, g, pn, lf);
       fence();
     });
+    PHASE(const unsigned c3 = PhaseClock::now(); ph.cyc_a += c1 - c0; ph.cyc_check += c2 - c1;
+          ph.cyc_b += c3 - c2; ++ph.tiles; fence();)
   };
   // A wavefront's last tile t: no S(t+1) and no exp2 of it; the exp2 of keys
   // 32-63 of S(t), the row-sum check and the PV(t) MFMAs as in tile().
@@ -396,6 +477,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
 
   wait_dma();
   __syncthreads();
+  PHASE(ph.rt_ready = PhaseClock::real();)
   if (nw > 0) {
     s_plain(s0);
     if (edge(0)) mask_tile(s0, 0);
@@ -405,6 +487,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
 #pragma unroll
     for (int g = 0; g < 8; ++g) exp_pair(s0, g, pf0, lf);
   }
+  PHASE(fence(); ph.rt_loop = PhaseClock::real(); ph.c_loop = PhaseClock::now(); fence();)
   // Iteration t: K(t+1) in K stage (t+1)&1, V(t) in V stage t&1; loads K(t+2)
   // into K stage t&1 and V(t+1) into V stage (t+1)&1, whose previous tiles
   // every wavefront has finished reading at the barrier.
@@ -412,10 +495,16 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   // loop, tile nw-1 by tile_last, then barrier-only iterations that keep
   // issuing the workgroup's loads.
   auto sync_load = [&](int t) {
+    PHASE(const unsigned c0 = PhaseClock::now(); fence();)
     wait_dma();
+    PHASE(fence(); const unsigned cw = PhaseClock::now(); fence();)
     __syncthreads();
+    PHASE(fence(); const unsigned cb = PhaseClock::now(); ph.cyc_vmwait += cw - c0; ph.cyc_barrier += cb - cw;
+          fence();)
     if (t + 2 < N) kload.load(t + 2, (t & 1) ? kst[1] : kst[0], wave);
+    PHASE(fence(); const unsigned ck = PhaseClock::now(); ph.cyc_dma_k += ck - cb; fence();)
     if (t + 1 < N) vload.load(t + 1, (t & 1) ? vst[0] : vst[1], wave);
+    PHASE(fence(); ph.cyc_sync += PhaseClock::now() - c0;)
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -443,11 +532,14 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       pf0[1] = pf1[1];
     }
     sync_load(last);
+    PHASE(const unsigned cl = PhaseClock::now(); fence();)
     tile_last(s0, pf0, (last & 1) * TB);
+    PHASE(fence(); ph.cyc_last += PhaseClock::now() - cl;)
     t = last + 1;
   }
   for (; t < N; ++t) sync_load(t);
 
+  PHASE(fence(); const unsigned c_epi = PhaseClock::now(); fence();)
   const float lt = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / lt;
   if (p.lse && half == 0 && qi < Tq) p.lse[(int64_t)bh * Tq + qi] = b_run + __log2f(lt);
@@ -463,6 +555,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
         *reinterpret_cast<bf16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
       }
   }
+  PHASE(fence(); ph.write(lane, id * kNW + wave, bh, mblk, N, nw, c_epi);)
 }
 
 template <int D, bool CAUSAL>
@@ -482,3 +575,23 @@ int launch_flash_bf16_pipe(const SdpaParams& p, hipStream_t s) {
 }
 
 }  // namespace mfx
+
+#if defined(MFX_PHASE_TIMERS)
+// Diagnostic build only: copies up to max_records phase records (16 u64 each,
+// fields as PhaseClock::write) to host memory after the device is idle and
+// returns how many the device array holds; clear != 0 zeroes the array
+// afterwards.  Not part of the product's C ABI.
+extern "C" __attribute__((visibility("default"))) int64_t mfx_phase_timers_read(void* host, int64_t max_records,
+                                                                                int clear) {
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  void* dev = nullptr;
+  if (hipGetSymbolAddress(&dev, HIP_SYMBOL(mfx::g_phase_records)) != hipSuccess) return -1;
+  const int64_t n = max_records < mfx::kPhaseRecords ? max_records : mfx::kPhaseRecords;
+  if (host && n > 0 &&
+      hipMemcpy(host, dev, (size_t)n * mfx::kPhaseFields * 8, hipMemcpyDeviceToHost) != hipSuccess)
+    return -1;
+  if (clear && hipMemset(dev, 0, sizeof(mfx::g_phase_records)) != hipSuccess) return -1;
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  return mfx::kPhaseRecords;
+}
+#endif

@@ -224,8 +224,10 @@ def ew_program(dims, inputs, code, result, out_dtype=MFX_F32):
 _lib = None
 
 
-def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
-    """Loads libmfx_kernels.so (once) and declares its signatures."""
+def load(path: str | os.PathLike | None = None, make_default: bool = False) -> ctypes.CDLL:
+    """Loads libmfx_kernels.so (once) and declares its signatures.  A `path`
+    loads that copy instead (for example the phase-timer build); with
+    make_default the module's calls use it from then on."""
     global _lib
     if _lib is not None and path is None:
         return _lib
@@ -274,7 +276,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.mfx_gemm_ew_source.restype = ctypes.c_int64
     lib.mfx_elementwise.argtypes = [ctypes.POINTER(EwProgram), ctypes.c_void_p]
     lib.mfx_elementwise.restype = ctypes.c_int
-    if path is None:
+    if path is None or make_default:
         _lib = lib
     return lib
 

@@ -1,0 +1,169 @@
+"""Per-tile time budget of the pipelined bf16 flash kernel on config 3.
+
+    python jax-mlx-plugin_amd/build.py phase_timers
+    python jax-mlx-plugin_amd/phase_budget.py [--json out.json]
+
+Loads the diagnostic copy of libmfx_kernels.so built with -DMFX_PHASE_TIMERS
+(jax_mlx_amd/lib/phase_timers/), runs causal bf16 SDPA on config 3's inputs
+([4, 32, 2048, 128], numpy default_rng(3)), and reads the per-wavefront phase
+records the kernel writes (sdpa_flash_bf16_pipe.hip, PhaseClock):
+
+- the shader clock under this load (s_memtime cycles over s_memrealtime);
+- cycles per 64-key tile and wavefront in each phase of the loop -- A: the S
+  MFMAs of the next tile with the exp2 of this one, C: the row-sum check,
+  B: the PV MFMAs with the next tile's exp2, S: barrier plus the next tiles'
+  DMA issue -- against the MFMA floor (two wavefronts per SIMD, 32 MFMAs
+  each per tile, 32 cycles per v_mfma_f32_32x32x16_bf16);
+- per-block start (first tiles landed, loop entry), last tile and epilogue;
+- SIMD occupancy over the kernel span and the spread between XCDs.
+
+The instrumented kernel runs a few percent slower than the shipped one (a
+handful of s_memtime reads per tile); shares of the budget are what it is for.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB = PKG / "jax_mlx_amd" / "lib" / "phase_timers" / "libmfx_kernels.so"
+RT_HZ = 100e6          # s_memrealtime frequency
+MFMA_CYCLES = 32       # v_mfma_f32_32x32x16_bf16 issue-to-issue on one SIMD
+MFMAS_PER_TILE = 32    # per wavefront and 64-key tile at d = 128: 16 for S, 16 for PV
+WAVES_PER_SIMD = 2
+FIELDS = 20             # u64 per wavefront record (PhaseClock, kPhaseFields)
+
+
+def run(steps: int, lib_path: Path = LIB):
+    import ctypes
+
+    import torch
+
+    sys.path.insert(0, str(PKG))
+    from jax_mlx_amd import native
+
+    lib = native.load(lib_path, make_default=True)
+    lib.mfx_phase_timers_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    lib.mfx_phase_timers_read.restype = ctypes.c_int64
+    B, H, T, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(3)
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32)).cuda().bfloat16()
+               for _ in range(3))
+    out = torch.empty_like(q)
+    call = lambda: native.sdpa(q, k, v, scale=d ** -0.5, causal=True, out=out)  # noqa: E731
+    # Clocks rise under sustained load: 0.25 s of launches first.
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.25:
+        for _ in range(10):
+            call()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    avg_us = e0.elapsed_time(e1) * 1e3 / steps
+    cap = lib.mfx_phase_timers_read(None, 0, 1)   # clear
+    call()
+    n = 2048 * 4
+    rec = np.zeros((n, FIELDS), dtype=np.uint64)
+    got = lib.mfx_phase_timers_read(rec.ctypes.data, n, 0)
+    if got < 0 or cap < n:
+        raise RuntimeError("reading the phase records failed")
+    return rec, avg_us
+
+
+def budget(rec: np.ndarray, avg_us: float) -> dict:
+    rec = rec[rec[:, 4] != 0]
+    if not len(rec):
+        raise RuntimeError("no phase records written: the kernel that ran was not the phase-timer build")
+    ids, rt_end = rec[:, 0], rec[:, 4].astype(np.int64)
+    lo = lambda f: ((rec[:, 4] & 0xffffffff).astype(np.int64) - rec[:, f].astype(np.int64)) % (1 << 32)  # noqa
+    rt_start = rt_end - lo(1)
+    rt_ready = rt_end - lo(2)
+    rt_loop = rt_end - lo(3)
+    cyc = {name: rec[:, f].astype(np.float64) for name, f in
+           (("A", 5), ("C", 6), ("B", 7), ("S", 8), ("last", 9), ("total", 12), ("pre", 13), ("epi", 15),
+            ("S_vmwait", 16), ("S_barrier", 17), ("S_dma_k", 18))}
+    tiles = rec[:, 10].astype(np.float64)
+    rebases = int(rec[:, 11].sum())
+    dur_s = (rt_end - rt_start) / RT_HZ
+    clock_mhz = np.median(cyc["total"] / dur_s) / 1e6
+    t0 = rt_start.min()
+    span_us = (rt_end.max() - t0) / RT_HZ * 1e6
+    per_tile = {p: float(cyc[p].sum() / tiles.sum()) for p in ("A", "C", "B", "S")}
+    loop_tile = sum(per_tile.values())
+    floor = MFMAS_PER_TILE * MFMA_CYCLES * WAVES_PER_SIMD
+    # SIMD occupancy: waves resident per SIMD over the kernel span.
+    xcc = (ids & 0xff).astype(np.int64)
+    hw = ((ids >> 8) & 0xffffffff).astype(np.int64)
+    simd = (xcc << 16) | (((hw >> 13) & 7) << 12) | (((hw >> 12) & 1) << 11) | (((hw >> 8) & 15) << 4) | \
+        ((hw >> 4) & 3)
+    occ = np.zeros(4)
+    for key in np.unique(simd):
+        m = simd == key
+        ev = sorted([(int(s), 1) for s in rt_start[m]] + [(int(e), -1) for e in rt_end[m]])
+        cur, last = 0, int(t0)
+        for tm, dlt in ev:
+            occ[min(cur, 3)] += tm - last
+            cur += dlt
+            last = tm
+        occ[0] += int(rt_end.max()) - last
+    occ /= occ.sum()
+    xcd_end = {int(x): (rt_end[xcc == x].max() - t0) / RT_HZ * 1e6 for x in np.unique(xcc)}
+    us = lambda a: float(np.median(a) / RT_HZ * 1e6)  # noqa: E731
+    return {
+        "kernel_avg_us_instrumented": round(avg_us, 2),
+        "span_us": round(span_us, 2),
+        "shader_clock_mhz": round(float(clock_mhz), 1),
+        "wavefronts": int(len(rec)), "loop_tiles": int(tiles.sum()), "rebases": rebases,
+        "cycles_per_tile_per_wavefront": {**{k: round(v, 1) for k, v in per_tile.items()},
+                                          "sum": round(loop_tile, 1)},
+        "barrier_phase_split_per_tile": {
+            "vmcnt_wait": round(float(cyc["S_vmwait"].sum() / tiles.sum()), 1),
+            "s_barrier": round(float(cyc["S_barrier"].sum() / tiles.sum()), 1),
+            "dma_issue": round(float((cyc["S"] - cyc["S_vmwait"] - cyc["S_barrier"]).sum() / tiles.sum()), 1),
+            "dma_issue_k_tile": round(float(cyc["S_dma_k"].sum() / tiles.sum()), 1),
+            "note": "sums over every barrier a wavefront passes (loop tiles, its last tile, barrier-only "
+                    "iterations) divided by its loop tiles"},
+        "mfma_floor_cycles_per_tile_per_simd": floor,
+        "loop_mfma_fraction": round(floor / loop_tile, 4),
+        "median_us_start_to_first_tiles": round(us(rt_ready - rt_start), 3),
+        "median_us_start_to_loop": round(us(rt_loop - rt_start), 3),
+        "median_us_start_to_loop_first_blocks": round(us((rt_loop - rt_start)[rt_start - t0 < 2 * RT_HZ * 1e-6]), 3),
+        "median_us_start_to_loop_later_blocks": round(us((rt_loop - rt_start)[rt_start - t0 >= 2 * RT_HZ * 1e-6]), 3),
+        "median_cycles_last_tile": float(np.median(cyc["last"])),
+        "median_cycles_epilogue": float(np.median(cyc["epi"])),
+        "simd_occupancy_fraction_0_1_2_3plus_waves": [round(float(x), 4) for x in occ],
+        "xcd_finish_us": {k: round(v, 2) for k, v in sorted(xcd_end.items())},
+        "xcd_finish_spread_us": round(max(xcd_end.values()) - min(xcd_end.values()), 2),
+        "share_of_wavefront_cycles": {
+            p: round(float(cyc[p].sum() / cyc["total"].sum()), 4) for p in ("pre", "A", "C", "B", "S", "last", "epi")},
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--json", help="also write the budget here")
+    ap.add_argument("--lib", type=Path, default=LIB, help="a phase-timer build of libmfx_kernels.so")
+    args = ap.parse_args()
+    if not args.lib.exists():
+        print(f"{args.lib} is not built: python jax-mlx-plugin_amd/build.py phase_timers", file=sys.stderr)
+        return 1
+    rec, avg_us = run(args.steps, args.lib)
+    b = budget(rec, avg_us)
+    print(json.dumps(b, indent=1))
+    if args.json:
+        Path(args.json).write_text(json.dumps(b, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
