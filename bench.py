@@ -154,6 +154,33 @@ def bench_config3(torch, native, steps, warmup):
     }
 
 
+def bench_masked_prefill(torch, native, steps, warmup):
+    """Prefill with an additive padding mask: bf16 [4,32,2048,128], non-causal,
+    f32 mask [4,1,1,2048] = 0 / -inf by per-batch lengths from
+    default_rng(3) (drawn after q, k, v), beside the same call without a
+    mask.  TFLOP/s on the full (unmasked) FLOP count 4*B*H*T*T*d for both."""
+    import numpy as np
+
+    B, H, T, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(3)
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32)).to("cuda").bfloat16()
+               for _ in range(3))
+    lens = rng.integers(T // 2, T, size=B, endpoint=True)
+    mask = torch.from_numpy(np.where(np.arange(T)[None] < lens[:, None], 0.0, -np.inf)
+                            .reshape(B, 1, 1, T).astype(np.float32)).cuda()
+    out = torch.empty_like(q)
+    flops = 4.0 * B * H * T * T * d
+    res = {"shape": [B, H, T, d], "mask": "f32 [4,1,1,2048] padding, lengths " + ",".join(map(str, lens))}
+    for name, m in (("masked", mask), ("mask_free", None)):
+        avg_ms, med_ms, _ = time_launches(
+            torch, lambda: native.sdpa(q, k, v, scale=d ** -0.5, mask=m, out=out), steps, warmup)
+        res[name] = {"avg_us": avg_ms * 1e3, "median_us": med_ms * 1e3,
+                     "TFLOPs": flops / (avg_ms * 1e-3) / 1e12,
+                     "kernel": native.sdpa_kernel_name(q, k, v, mask=m)}
+    res["masked_over_mask_free"] = res["masked"]["avg_us"] / res["mask_free"]["avg_us"]
+    return res
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -564,6 +591,7 @@ ONLY = {
         "sweep": [bench_layer_norm(torch, native, 1 << 20, 512, k, w),
                   bench_layer_norm(torch, native, 65536, 4096, k, w)]},
     "copy": lambda torch, native, k, w: bench_copy(torch, k, w),
+    "masked_prefill": lambda torch, native, k, w: bench_masked_prefill(torch, native, k, w),
     "pjrt": lambda torch, native, k, w: {
         "config3_pjrt": bench_sdpa_pjrt(torch, 3, k, w, bench_config3(torch, native, k, w)["avg_ms"] * 1e3),
         "config5_pjrt": bench_sdpa_pjrt(torch, 5, k, w, bench_config5(torch, native, k, w)["avg_us"])},
@@ -662,6 +690,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("config 2: SDPA f32 [8,8,128,64]")
         extra["config2_sdpa_f32"] = bench_config2(torch, native, 200, 20)
+        log("masked prefill: padding mask [4,1,1,2048] on [4,32,2048,128] bf16")
+        extra["masked_prefill"] = bench_masked_prefill(torch, native, 20, 3)
+        torch.cuda.empty_cache()
         log("config 5: GQA decode bf16 + RMSNorm(q)")
         extra["config5_decode"] = bench_config5(torch, native, 50, 5)
         torch.cuda.empty_cache()

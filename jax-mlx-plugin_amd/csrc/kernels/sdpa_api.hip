@@ -70,6 +70,7 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
   p.dtype = a->dtype;
   p.causal = a->causal ? 1 : 0;
   p.scale_log2 = a->scale * kLog2e;
+  p.inv_scale_log2 = p.scale_log2 != 0.f ? 1.f / p.scale_log2 : 0.f;
   p.q_rms_eps = a->q_rms_eps;
   p.num_splits = 1;
   p.split_len = p.Tk;

@@ -284,6 +284,7 @@ int make_bwd_plan(const mfx_sdpa_bwd_args* a, BwdPlan& out) {
   f.dtype = p.dtype;
   f.causal = p.causal;
   f.scale_log2 = p.scale_log2;
+  f.inv_scale_log2 = p.scale_log2 != 0.f ? 1.f / p.scale_log2 : 0.f;
   f.q_rms_eps = -1.f;
   f.num_splits = 1;
   f.split_len = p.Tk;

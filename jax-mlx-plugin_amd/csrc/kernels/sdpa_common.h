@@ -21,6 +21,7 @@ struct SdpaParams {
   int dtype;
   int causal;
   float scale_log2;  // scale * log2(e)
+  float inv_scale_log2;  // 1 / scale_log2 (0 when scale_log2 is 0)
   float q_rms_eps;   // < 0: no RMSNorm on q
   int num_splits;    // split-KV decode only: partials per row
   int split_len;     // keys per split (VALU decode; the MFMA decode interleaves tiles)

@@ -316,9 +316,10 @@ bool flash_bf16_supports(const SdpaParams& p) {
 }
 
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s) {
-  // Without an additive mask the software-pipelined kernel runs
-  // (sdpa_flash_bf16_pipe.hip); this file's kernel serves masked calls.
-  if (!p.mask) return launch_flash_bf16_pipe(p, s);
+  // Without an additive mask, or with one that does not vary along query
+  // rows, the software-pipelined kernel runs (sdpa_flash_bf16_pipe.hip);
+  // this file's kernel serves masks with a query-row stride.
+  if (!p.mask || p.ms[2] == 0) return launch_flash_bf16_pipe(p, s);
   if (p.D == 128) return launch_d<128>(p, s);
   return launch_d<64>(p, s);
 }

@@ -31,7 +31,19 @@
 // A wavefront's last tile runs outside the loop (tile_last: no S of a next
 // tile), its registers moved to the even-tile set and its V stage a runtime
 // offset, so the loop keeps its two tile bodies and the kernel stays
-// spill-free.  No spill is allowed here: the inline-asm LDS reads complete
+// spill-free.
+//
+// MT != 0 adds an additive mask that does not vary along query rows (element
+// strides [b, h, 0, key]: padding masks, per-head key biases) of type f32
+// (MT 1), bf16 (2) or f16 (3).  Wavefront 0 loads a tile's 64 values one
+// tile ahead (one lane per key, issued with the K DMA), converts them to raw
+// score units (mask_log2 / (scale * log2 e), finite values held at or above
+// -2^30 in log2 units, -inf kept) and writes them to a 64-float LDS row before the
+// barrier that publishes the tile.  The S products of the tile start from
+// that row instead of zero (the MFMA's accumulator input), so S comes out as
+// Q K^T + mask / (scale * log2 e) and the exp2, row-max, rebase and row-sum
+// code runs unchanged, with no vector work for the mask.  Masks that vary
+// along query rows run on the kernel of sdpa_flash_bf16.hip.  No spill is allowed here: the inline-asm LDS reads complete
 // after the asm statement, and a spill or copy of a destination register
 // placed before its lgkmcnt wait would save the value before it arrives.
 //
@@ -174,20 +186,28 @@ struct Loader {
   }
 };
 
-// lgkmcnt of the wait before S MFMA j (MS per tile, reads kPfK ahead) and
-// before PV MFMA j (MP per tile, read pairs kPfV ahead): the reads issued
+// lgkmcnt of the wait before S MFMA j (MS per tile, reads pf ahead) and
+// before PV MFMA j (MP per tile, read pairs pf ahead): the reads issued
 // after the one the MFMA needs.
-constexpr int wait_k(int j, int MS) { return kPfK < MS - 1 - j ? kPfK : MS - 1 - j; }
-constexpr int wait_v(int j, int MP) { return 2 * (kPfV < MP - 1 - j ? kPfV : MP - 1 - j); }
+constexpr int wait_k(int j, int MS, int pf) { return pf < MS - 1 - j ? pf : MS - 1 - j; }
+constexpr int wait_v(int j, int MP, int pf) { return 2 * (pf < MP - 1 - j ? pf : MP - 1 - j); }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int MT>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   constexpr int TILE = kBN * D;     // elements of one K or V tile
   constexpr int TB = TILE * 2;      // its bytes
   constexpr int MS = 2 * (D / 16);  // S MFMAs per tile
   constexpr int MP = 4 * (D / 32);  // PV MFMAs per tile
+  constexpr bool MASK = MT != 0;
+  // Operand reads ahead of their MFMA: 2, 4 and 6 measured alike on config
+  // 3; a masked kernel keeps 2 for the registers its mask rows take.
+  constexpr int PFK = MASK ? 2 : kPfK, PFV = MASK ? 2 : kPfV;
   static_assert(MS % 8 == 0 || 8 % MS == 0, "interleave");
   __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 K1 V0 V1
+  // Mask rows (raw score units) of the tiles in K stages 0 / 1 (MASK only):
+  // an array of its own, so the compiler's reads of it need no wait for the
+  // K/V DMA into smem.
+  __shared__ __attribute__((aligned(16))) float mrow_lds[MASK ? 2 : 1][kBN];
 
   PHASE(PhaseClock ph;)
   const int tid = threadIdx.x;
@@ -221,6 +241,52 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   bf16* op = static_cast<bf16*>(p.out) + b * p.os[0] + h * p.os[1];
   const int64_t qs2 = p.qs[2], os2 = p.os[2];
   const int Tq = p.Tq, Tk = p.Tk;
+  // Mask row of this (batch, head): element offset of key 0 (MASK only).
+  const int64_t mrow = MASK ? b * p.ms[0] + h * p.ms[1] : 0;
+  // Raw mask value of key t*kBN + lane (keys past Tk read the last key's:
+  // they are masked per element anyway).
+  // The lane index goes through an opaque copy here and in mask_store, so
+  // the per-lane addresses are formed at each use rather than hoisted and
+  // kept in registers across the loop (they serve wavefront 0 only).
+  auto mask_raw = [&](int t) -> float {
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    const int64_t key = min(t * kBN + l, Tk - 1);
+    if constexpr (MASK) return load_mask_t<MT>(p.mask, mrow + key * p.ms[3]);
+    return 0.f;
+  };
+  // Wavefront 0: converts a raw mask value to score units and stores it as
+  // key `lane` of mask row `stage`: log2 units held at or above -2^30, then
+  // divided by scale * log2(e); -inf stays -inf.  The floor outweighs any
+  // score (a key at it gets weight 0 beside a real one) and is absorbed by
+  // the scores it is added to (|s * scale * log2 e| <= 64), so keys at it
+  // hold equal S values; and since |floor| < 2^31 the exp2 FMA's rounding
+  // residual stays below 64, the same for equal S values: a row whose keys
+  // all carry the floor (JAX's finite -0.7 * FLT_MAX mask) gets equal finite
+  // weights, the mean of V, where the softmax of where(mask, s, floor) does.
+  const float inv_sl2 = p.inv_scale_log2;
+  auto mask_store = [&](float raw, int stage) {
+    if constexpr (MASK) {
+      int l = lane;
+      asm volatile("" : "+v"(l));
+      const float m = mask_log2(raw);
+      mrow_lds[stage][l] = m == -INFINITY ? m : fmaxf(m, -1073741824.f) * inv_sl2;
+    }
+  };
+  // Accumulator seed of S chain mt (32-key block) for the tile in `stage`:
+  // element i is key mt*32 + (i/4)*8 + half*4 + i%4 of the row.
+  auto mask_seed = [&](int stage, int mt) -> f32x16 {
+    f32x16 r = {};
+    if constexpr (MASK) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4 m = *reinterpret_cast<const f32x4*>(&mrow_lds[stage][mt * 32 + g4 * 8 + half * 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[g4 * 4 + e] = m[e];
+      }
+    }
+    return r;
+  };
 
   const int q0 = mblk * kBM + wave * 32;  // first query row of this wavefront (uniform)
   const int qi = q0 + l32;
@@ -240,6 +306,12 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   const Loader<D> kload(kp, p.ks[2], Tk, wave, lane), vload(vp, p.vs[2], Tk, wave, lane);
   bf16* const kst[2] = {smem, smem + TILE};
   bf16* const vst[2] = {smem + 2 * TILE, smem + 3 * TILE};
+  // Raw mask value of the next tile wavefront 0 converts at the next barrier.
+  float mraw = 0.f;
+  if (MASK && wave == 0 && N > 0) {
+    mask_store(mask_raw(0), 0);
+    if (N > 1) mraw = mask_raw(1);
+  }
   if (N > 0) {
     kload.load(0, kst[0], wave);
     if (N > 1) kload.load(1, kst[1], wave);
@@ -343,8 +415,17 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   auto rebase = [&](f32x16 (&sc)[2], u32x4 (&pc)[2]) -> float {
     const float rel = row_max(sc) * sl2 - b_run;
     const float d = rel > kSlack ? rel : 0.f;
-    const float alpha = __builtin_amdgcn_exp2f(-d);
-    b_run += d;
+    float alpha;
+    if constexpr (MASK) {
+      // Scores at the mask floor sit near -2^30 in log2 units, where b_run + d
+      // can round back to b_run: scale by the change that happened.
+      const float nb = b_run + d;
+      alpha = __builtin_amdgcn_exp2f(b_run - nb);
+      b_run = nb;
+    } else {
+      alpha = __builtin_amdgcn_exp2f(-d);
+      b_run += d;
+    }
     nbase = -b_run;
     l_run *= alpha;
 #pragma unroll
@@ -370,9 +451,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
 #pragma unroll
     for (int j = 0; j < MS; ++j) lgkm_tie<0>(kr[j]);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[mt][i] = 0.f;
+    for (int mt = 0; mt < 2; ++mt) s[mt] = mask_seed(0, mt);
 #pragma unroll
     for (int j = 0; j < MS; ++j) s[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], s[j & 1], 0, 0, 0);
   };
@@ -401,16 +480,22 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     };
     float ls = 0.f;
     PHASE(const unsigned c0 = PhaseClock::now(); fence();)
-    static_for<0, kPfK>(rdk);
+    // S(t+1) starts from tile t+1's mask row (zero without a mask); the
+    // second chain's seed is read once the first MFMA is issued.
+    const f32x16 seed0 = mask_seed((t + 1) & 1, 0);
+    f32x16 seed1 = {};
+    static_for<0, PFK>(rdk);
     fence();
     static_for<0, MS>([&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
-      if constexpr (j + kPfK < MS) rdk(std::integral_constant<int, j + kPfK>{});
-      lgkm_tie<wait_k(j, MS)>(kr[j]);
-      if constexpr (j < 2)
-        sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], f32x16{}, 0, 0, 0);
-      else
+      if constexpr (j + PFK < MS) rdk(std::integral_constant<int, j + PFK>{});
+      lgkm_tie<wait_k(j, MS, PFK)>(kr[j]);
+      if constexpr (j < 2) {
+        sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], j ? seed1 : seed0, 0, 0, 0);
+        if constexpr (MASK && j == 0) seed1 = mask_seed((t + 1) & 1, 1);
+      } else {
         sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], sn[j & 1], 0, 0, 0);
+      }
 #pragma unroll
       for (int g = 8 + j * 8 / MS; g < 8 + (j + 1) * 8 / MS; ++g) exp_pair(sc, g, pb, ls);
       fence();
@@ -425,13 +510,13 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     l_run += lt;
     lf = 0.f;
     PHASE(fence(); const unsigned c2 = PhaseClock::now(); fence();)
-    static_for<0, kPfV>(rdv);
+    static_for<0, PFV>(rdv);
     fence();
     static_for<0, MP>([&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
       constexpr int dt = j % (D / 32), ks = j / (D / 32);
-      if constexpr (j + kPfV < MP) rdv(std::integral_constant<int, j + kPfV>{});
-      lgkm_tie<wait_v(j, MP)>(vr[j][0], vr[j][1]);
+      if constexpr (j + PFV < MP) rdv(std::integral_constant<int, j + PFV>{});
+      lgkm_tie<wait_v(j, MP, PFV)>(vr[j][0], vr[j][1]);
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
       const u32x4 pbk = ks < 2 ? pc[ks & 1] : pb[ks & 1];
@@ -453,7 +538,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       ds_tr<2 * TB + ks * 16 * D * 2>(vr[j][0], va[dt][0] + vs_bytes);
       ds_tr<2 * TB + ks * 16 * D * 2>(vr[j][1], va[dt][1] + vs_bytes);
     };
-    static_for<0, kPfV>(rdv);
+    static_for<0, PFV>(rdv);
     fence();
     float ls = 0.f;
 #pragma unroll
@@ -465,8 +550,8 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     static_for<0, MP>([&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
       constexpr int dt = j % (D / 32), ks = j / (D / 32);
-      if constexpr (j + kPfV < MP) rdv(std::integral_constant<int, j + kPfV>{});
-      lgkm_tie<wait_v(j, MP)>(vr[j][0], vr[j][1]);
+      if constexpr (j + PFV < MP) rdv(std::integral_constant<int, j + PFV>{});
+      lgkm_tie<wait_v(j, MP, PFV)>(vr[j][0], vr[j][1]);
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
       const u32x4 pbk = ks < 2 ? pc[ks & 1] : pb[ks & 1];
@@ -497,8 +582,12 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   auto sync_load = [&](int t) {
     PHASE(const unsigned c0 = PhaseClock::now(); fence();)
     wait_dma();
+    // Wavefront 0 publishes mask row t+1 with this barrier (its stage held
+    // row t-1, last read before the previous barrier).
+    if (MASK && wave == 0 && t + 1 < N) mask_store(mraw, (t + 1) & 1);
     PHASE(fence(); const unsigned cw = PhaseClock::now(); fence();)
     __syncthreads();
+    if (MASK && wave == 0 && t + 2 < N) mraw = mask_raw(t + 2);
     PHASE(fence(); const unsigned cb = PhaseClock::now(); ph.cyc_vmwait += cw - c0; ph.cyc_barrier += cb - cw;
           fence();)
     if (t + 2 < N) kload.load(t + 2, (t & 1) ? kst[1] : kst[0], wave);
@@ -558,20 +647,39 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   PHASE(fence(); ph.write(lane, id * kNW + wave, bh, mblk, N, nw, c_epi);)
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int MT>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   const int nmb = (p.Tq + kBM - 1) / kBM;
   const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
-  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, CAUSAL>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
+  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, CAUSAL, MT>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
   return launch_status("flash_bf16_pipe_kernel");
+}
+
+template <int D, int MT>
+int launch_c(const SdpaParams& p, hipStream_t s) {
+  return p.causal ? launch_t<D, true, MT>(p, s) : launch_t<D, false, MT>(p, s);
+}
+
+template <int D>
+int launch_m(const SdpaParams& p, hipStream_t s) {
+  if (!p.mask) return launch_c<D, 0>(p, s);
+#if defined(MFX_PHASE_TIMERS)
+  // The diagnostic build instruments the mask-free kernels only.
+  return fail(MFX_E_UNSUPPORTED, "phase-timer build: masked attention is not instrumented");
+#else
+  if (p.mask_dtype == MFX_F32) return launch_c<D, 1>(p, s);
+  if (p.mask_dtype == MFX_BF16) return launch_c<D, 2>(p, s);
+  return launch_c<D, 3>(p, s);
+#endif
 }
 
 }  // namespace
 
-// Mask-free flash attention (the caller checked flash_bf16_supports).
+// Flash attention without an additive mask or with one that does not vary
+// along query rows, p.ms[2] == 0 (the caller checked flash_bf16_supports).
 int launch_flash_bf16_pipe(const SdpaParams& p, hipStream_t s) {
-  if (p.D == 128) return p.causal ? launch_t<128, true>(p, s) : launch_t<128, false>(p, s);
-  return p.causal ? launch_t<64, true>(p, s) : launch_t<64, false>(p, s);
+  if (p.D == 128) return launch_m<128>(p, s);
+  return launch_m<64>(p, s);
 }
 
 }  // namespace mfx

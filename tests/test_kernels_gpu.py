@@ -298,6 +298,72 @@ def test_sdpa_btnh_layout_gqa_and_mask(cuda, nat, oracle, dtype):
 
 
 @pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mdt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("kind", ["padding", "head_bias"])
+def test_sdpa_flash_bf16_row_shared_mask(cuda, nat, oracle, D, mdt, causal, kind):
+    """Additive masks that do not vary along query rows run on the pipelined
+    bf16 kernel (the mask row seeds the S accumulators).  padding: [B,1,1,Tk]
+    0 / -inf by sequence length, one batch with whole masked 64-key tiles;
+    head_bias: [B,H,1,Tk] N(0,1) biases with -inf holes and a masked run.
+    Ragged Tq / Tk, GQA, every mask dtype, causal or not, against the oracle."""
+    td = cuda.bfloat16
+    rng = np.random.default_rng(40 + D)
+    B, Hq, Hkv, Tq, Tk = 2, 4, 2, 200, 333
+    q, k, v = make_qkv(cuda, 41, (B, Hq, Tq, D), (B, Hkv, Tk, D), td)
+    if kind == "padding":
+        lens = np.array([Tk, 150])
+        mask = np.where(np.arange(Tk)[None] < lens[:, None], 0.0, -np.inf).reshape(B, 1, 1, Tk)
+    else:
+        mask = rng.standard_normal((B, Hq, 1, Tk))
+        mask[rng.random(mask.shape) < 0.1] = -np.inf
+        mask[:, :, :, 64:128] = -np.inf          # a whole masked tile
+        mask[:, :, :, 0] = 0.0                   # every row keeps key 0
+    mdev = {"f32": cuda.float32, "bf16": cuda.bfloat16, "f16": cuda.float16}[mdt]
+    maskd = dev(cuda, mask, cuda.float32).to(mdev)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd, causal=causal) == f"flash_bf16_d{D}"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, mask=maskd, causal=causal)
+    ref = oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=causal, mask=host(maskd))
+    check_sdpa(out, ref, "bf16")
+
+
+def test_sdpa_flash_bf16_row_shared_mask_all_inf_is_nan(cuda, nat, oracle):
+    """A row-shared mask that is -inf on every key of one batch: that batch's
+    rows are 0/0 (NaN, as exp(x - max) / sum gives); the other batch matches
+    the oracle."""
+    q, k, v = make_qkv(cuda, 42, (2, 4, 130, 128), (2, 4, 200, 128), cuda.bfloat16)
+    mask = np.zeros((2, 1, 1, 200))
+    mask[1] = -np.inf
+    maskd = dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd) == "flash_bf16_d128"
+    out = nat.sdpa(q, k, v, scale=0.1, mask=maskd).float()
+    assert bool(cuda.isnan(out[1]).all())
+    ref = oracle.sdpa(host(q[:1]), host(k[:1]), host(v[:1]), 0.1)
+    check_sdpa(out[:1], ref, "bf16")
+
+
+def test_sdpa_flash_bf16_padding_mask_config3_size(cuda, nat, oracle):
+    """The bench's masked prefill: [4,32,2048,128] bf16, non-causal, an f32
+    padding mask [4,1,1,2048] with lengths from default_rng(3); eight heads
+    (one per XCD residue and group slot) against the oracle, every output
+    finite, and padded-out keys never reach the output (equal to the same
+    heads run on keys cut to the batch's length)."""
+    from config3_heads import CONFIG3_HEADS
+
+    q, k, v = make_qkv(cuda, 3, (4, 32, 2048, 128), (4, 32, 2048, 128), cuda.bfloat16)
+    lens = np.random.default_rng(3).integers(1024, 2048, size=4, endpoint=True)
+    mask = np.where(np.arange(2048)[None] < lens[:, None], 0.0, -np.inf).reshape(4, 1, 1, 2048)
+    maskd = dev(cuda, mask, cuda.float32)
+    out = nat.sdpa(q, k, v, scale=128 ** -0.5, mask=maskd)
+    cuda.cuda.synchronize()
+    assert bool(cuda.isfinite(out.float()).all())
+    for b, h in CONFIG3_HEADS:
+        sl = lambda t: host(t[b:b + 1, h:h + 1])
+        ref = oracle.sdpa(sl(q), sl(k)[:, :, :lens[b]], sl(v)[:, :, :lens[b]], 128 ** -0.5)
+        check_sdpa(out[b:b + 1, h:h + 1], ref, "bf16")
+
+
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("case", ["growing", "spike", "shrinking", "wide_scale"])
 @pytest.mark.parametrize("causal", [False, True])
 def test_sdpa_flash_bf16_rebase(cuda, nat, oracle, D, case, causal):
@@ -553,7 +619,8 @@ def select_semantics_ref(oracle, q, k, v, scale, keep):
     return ref
 
 
-@pytest.mark.parametrize("case", ["flash_bf16_d128", "flash_f32_split_d64", "flash_f32_split_d128", "flash_f32_d64",
+@pytest.mark.parametrize("case", ["flash_bf16_d128", "flash_bf16_d128_shared", "flash_f32_split_d64",
+                                  "flash_f32_split_d128", "flash_f32_d64",
                                   "flash_f32_d128", "generic",
                                   "decode_splitkv_mfma",
                                   "decode_splitkv", "decode_splitkv_mfma_shared"])
@@ -563,6 +630,7 @@ def test_sdpa_finite_mask_fully_masked_rows(cuda, nat, oracle, case, mdt):
     of a row returns the mean of V (select semantics), not NaN: the kernels
     keep log2(e) * mask finite."""
     shapes = {"flash_bf16_d128": ((2, 4, 64, 128), (2, 2, 300, 128), "bf16"),
+              "flash_bf16_d128_shared": ((2, 4, 150, 128), (2, 2, 500, 128), "bf16"),
               "flash_f32_split_d64": ((2, 4, 64, 64), (2, 2, 200, 64), "f32"),
               "flash_f32_split_d128": ((2, 4, 64, 128), (2, 2, 200, 128), "f32"),
               "flash_f32_d64": ((16, 32, 128, 64), (16, 16, 200, 64), "f32"),  # 512 workgroups
