@@ -172,8 +172,12 @@ size_t mfx_layer_norm_bwd_workspace_size(const mfx_norm_bwd_args* args);
  *
  * workspace: split-KV decode keeps per-split partial results there.  Query
  * the size with mfx_sdpa_workspace_size(); pass NULL to let the library use a
- * per-device buffer it allocates once and reuses (calls that overlap on one
- * device then serialise on that buffer's stream order).
+ * buffer of its own for this device and stream (calls on one stream share it
+ * in stream order, calls on different streams get different buffers; when it
+ * must grow the library allocates a larger one and keeps the old one until
+ * the process ends, so it neither waits nor frees memory queued work may
+ * read, but it does call hipMalloc: callers that cannot allocate pass a
+ * workspace or use mfx_sdpa_fwd_noalloc).
  *
  * Replaces mlx::core::fast::scaled_dot_product_attention (reference
  * src/jax_mlx_pjrt.cpp:4444 for mlx.sdpa, :8138 for custom_call @mlx_sdpa).

@@ -38,10 +38,14 @@ inline int dtype_size(int dt) {
   }
 }
 
-// Per-device scratch buffer owned by the library (grown on demand, never
-// shrunk, freed at process exit).  Returns nullptr and sets the error on
-// failure.
-void* device_scratch(size_t bytes);
+// Scratch buffer owned by the library for the current device and `stream`
+// (so calls on different streams never share one): grown on demand by
+// replacing it, the old buffer kept until the process ends, so work queued
+// earlier stays valid and nothing waits.  Calls on one stream share it in
+// stream order.  Growing allocates (hipMalloc): a caller that cannot, such as
+// one capturing a graph, passes a workspace or uses mfx_sdpa_fwd_noalloc.
+// Returns nullptr and sets the error on failure.
+void* device_scratch(size_t bytes, hipStream_t stream);
 
 // Compute units of the current device (cached per device; 256 if the query
 // fails).

@@ -424,7 +424,7 @@ int mfx_layer_norm_bwd(const mfx_norm_bwd_args* args, void* stream) {
       if ((uintptr_t)a.workspace % 4) return fail(MFX_E_INVALID, "workspace must be 4-byte aligned");
       partial = static_cast<float*>(a.workspace);
     } else {
-      partial = static_cast<float*>(device_scratch(need));
+      partial = static_cast<float*>(device_scratch(need, s));
       if (!partial) return MFX_E_HIP;
     }
   }

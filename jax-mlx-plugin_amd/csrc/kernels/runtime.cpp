@@ -2,6 +2,7 @@
 // version queries.
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -25,15 +26,20 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 namespace {
+// Scratch of one (device, stream).  A buffer that grows is replaced, never
+// freed: work queued earlier may still read it, and freeing it would need a
+// synchronisation.  The retired buffers add up to less than the current one
+// (each replacement at least doubles) and live until the process ends.
 struct Scratch {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_scratch_mu;
-std::vector<Scratch> g_scratch;  // indexed by device ordinal
+std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
+std::vector<void*> g_retired;
 }  // namespace
 
-void* device_scratch(size_t bytes) {
+void* device_scratch(size_t bytes, hipStream_t stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -41,27 +47,18 @@ void* device_scratch(size_t bytes) {
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if ((size_t)dev >= g_scratch.size()) g_scratch.resize(dev + 1);
-  Scratch& s = g_scratch[dev];
+  Scratch& s = g_scratch[{dev, stream}];
   if (s.bytes >= bytes && s.ptr) return s.ptr;
-  if (s.ptr) {
-    // Work queued on any stream may still read the old buffer.
-    e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-      hip_fail(e, "hipDeviceSynchronize");
-      return nullptr;
-    }
-    (void)hipFree(s.ptr);
-    s.ptr = nullptr;
-    s.bytes = 0;
-  }
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-  e = hipMalloc(&s.ptr, want);
+  if (want < 2 * s.bytes) want = 2 * s.bytes;
+  void* p = nullptr;
+  e = hipMalloc(&p, want);
   if (e != hipSuccess) {
-    s.ptr = nullptr;
     hip_fail(e, "hipMalloc(scratch)");
     return nullptr;
   }
+  if (s.ptr) g_retired.push_back(s.ptr);
+  s.ptr = p;
   s.bytes = want;
   return s.ptr;
 }

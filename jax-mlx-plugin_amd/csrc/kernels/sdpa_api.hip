@@ -183,7 +183,7 @@ int mfx_sdpa_fwd(const mfx_sdpa_args* args, void* stream) {
         return fail(MFX_E_WORKSPACE, "workspace smaller than mfx_sdpa_workspace_size()");
       ws = static_cast<char*>(args->workspace);
     } else {
-      ws = static_cast<char*>(device_scratch(need));
+      ws = static_cast<char*>(device_scratch(need, s));
       if (!ws) return MFX_E_HIP;
     }
   }

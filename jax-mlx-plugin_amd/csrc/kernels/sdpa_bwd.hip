@@ -326,7 +326,7 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
     if ((uintptr_t)args->workspace % 256) return fail(MFX_E_INVALID, "workspace must be 256-byte aligned");
     ws = static_cast<char*>(args->workspace);
   } else {
-    ws = static_cast<char*>(device_scratch(need));
+    ws = static_cast<char*>(device_scratch(need, s));
     if (!ws) return MFX_E_HIP;
   }
   SdpaBwdParams& p = pl.p;

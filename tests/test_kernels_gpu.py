@@ -457,6 +457,33 @@ def test_sdpa_broadcast_kv_rows(cuda, nat, oracle, dtype, which):
         assert err <= (1e-5 if dtype == "f32" else 1e-2), err
 
 
+def test_sdpa_decode_library_scratch_per_stream(cuda, nat, oracle):
+    """Split-KV decodes without a workspace on two streams at once use the
+    library's scratch; each stream gets its own buffer, so the partials of
+    one call never overwrite the other's.  Repeated interleaved calls, the
+    second stream's problem larger (its buffer grows while the first stream
+    still has work queued), every result against the oracle."""
+    torch = cuda
+    qa, ka, va = make_qkv(cuda, 51, (4, 16, 1, 128), (4, 4, 3000, 128), cuda.bfloat16)
+    qb, kb, vb = make_qkv(cuda, 52, (8, 16, 1, 128), (8, 4, 6000, 128), cuda.bfloat16)
+    assert nat.sdpa_kernel_name(qa, ka, va) == "decode_splitkv_mfma"
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs_a, outs_b = [], []
+    for _ in range(4):
+        with torch.cuda.stream(sa):
+            outs_a.append(nat.sdpa(qa, ka, va, scale=0.1))
+        with torch.cuda.stream(sb):
+            outs_b.append(nat.sdpa(qb, kb, vb, scale=0.1))
+    torch.cuda.synchronize()
+    ref_a = oracle.sdpa(host(qa), host(ka), host(va), 0.1)
+    ref_b = oracle.sdpa(host(qb), host(kb), host(vb), 0.1)
+    for o in outs_a:
+        check_sdpa(o, ref_a, "bf16")
+    for o in outs_b:
+        check_sdpa(o, ref_b, "bf16")
+
+
 def test_sdpa_gqa_decode_golden(cuda, nat, golden):
     q, k, v = (dev(cuda, golden[f"gqa_{s}"], cuda.bfloat16) for s in "qkv")
     mask = dev(cuda, golden["gqa_mask"], cuda.float32)
