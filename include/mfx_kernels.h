@@ -48,8 +48,10 @@ int mfx_device_count(void);
 /*
  * Row normalisation over the last axis of a [rows, n] view.
  *   x / y     : rows spaced x_row_stride / y_row_stride elements apart,
- *               elements contiguous within a row; dtype `dtype`.
- *   gamma/beta: [n] vectors of `param_dtype`, each may be NULL.
+ *               elements contiguous within a row; dtype `dtype` (MFX_F32,
+ *               MFX_BF16 or MFX_F16; fp32 arithmetic).
+ *   gamma/beta: [n] vectors of `param_dtype` (any of the three), each may
+ *               be NULL.
  *   LayerNorm : y = (x - mean) / sqrt(var + eps) * gamma + beta, population
  *               variance computed two-pass in fp32 registers.
  *   RMSNorm   : y = x / sqrt(mean(x^2) + eps) * gamma  (beta ignored).
@@ -160,9 +162,9 @@ size_t mfx_layer_norm_bwd_workspace_size(const mfx_norm_bwd_args* args);
  * `dtype`, optionally times q_rms_weight[D] of `dtype`), which fuses the
  * RMSNorm(q) -> SDPA chain of GQA decode.  Pass a negative value to disable.
  *
- * dtype is MFX_F32 or MFX_BF16 (fp32 accumulation for both; bf16
- * probabilities feed the PV product in the bf16 path, as JAX's attention
- * casts them to the value dtype).
+ * dtype is MFX_F32, MFX_BF16 or MFX_F16 (fp32 accumulation for all; the
+ * 16-bit paths feed probabilities rounded to `dtype` to the PV product, as
+ * JAX's attention casts them to the value dtype).
  *
  * lse (optional output): the row log-sum-exp of the scaled, masked scores in
  * log2 units, lse[(b * Hq + h) * Tq + i] = log2(sum_j exp2(log2e * (scale *

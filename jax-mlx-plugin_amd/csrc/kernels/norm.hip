@@ -2,7 +2,7 @@
 // last axis.
 //
 // A row is owned by 16 or 64 lanes of one wavefront (rows up to 1024
-// 16-byte vectors, i.e. 4096 f32 / 8192 bf16 elements) or by a 256-thread
+// 16-byte vectors, i.e. 4096 f32 / 8192 bf16 or f16 elements) or by a 256-thread
 // workgroup (up to 4096 vectors); longer or unaligned rows take a looped
 // fallback.  Each element is read from HBM once and written once -- the HBM
 // roofline's algorithmic traffic.
@@ -236,8 +236,15 @@ int dispatch_typed(const mfx_norm_args& a, hipStream_t s) {
                        (a.y_row_stride % VEC == 0) &&
                        ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.y % 16 == 0) && params_aligned;
   const int64_t nvec = a.n / VEC;
-  if (aligned && nvec <= 4096) {
-    if (params && a.param_dtype == MFX_BF16) return dispatch_vec<T, bf16, OP>(a, s, nvec);
+  // Vector kernels read parameters stored as f32 or as bf16; f16 rows also
+  // take f16 parameters.  Other pairings run the looped kernel.
+  constexpr bool kF16 = std::is_same<T, _Float16>::value;
+  const bool pvec = !params || a.param_dtype == MFX_F32 || a.param_dtype == (kF16 ? MFX_F16 : MFX_BF16);
+  if (aligned && nvec <= 4096 && pvec) {
+    if (params && a.param_dtype != MFX_F32) {
+      if constexpr (kF16) return dispatch_vec<T, _Float16, OP>(a, s, nvec);
+      else return dispatch_vec<T, bf16, OP>(a, s, nvec);
+    }
     return dispatch_vec<T, float, OP>(a, s, nvec);
   }
   hipLaunchKernelGGL((row_kernel_looped<T, OP>), dim3((unsigned)a.rows), dim3(kBlock), 0, s,
@@ -256,15 +263,16 @@ int dispatch(const mfx_norm_args* a, void* stream) {
     return fail(MFX_E_INVALID, "row strides must be >= n");
   if (a->rows > 0x7fffffffLL) return fail(MFX_E_UNSUPPORTED, "too many rows");
   if (a->n > 0x7fffffffLL) return fail(MFX_E_UNSUPPORTED, "row too long");
-  if ((a->gamma || a->beta) && a->param_dtype != MFX_F32 && a->param_dtype != MFX_BF16)
-    return fail(MFX_E_UNSUPPORTED, "param_dtype must be f32 or bf16");
+  if ((a->gamma || a->beta) && a->param_dtype != MFX_F32 && a->param_dtype != MFX_BF16 && a->param_dtype != MFX_F16)
+    return fail(MFX_E_UNSUPPORTED, "param_dtype must be f32, bf16 or f16");
   if (!is_softmax(OP) && !(a->eps >= 0.f))
     return fail(MFX_E_INVALID, "eps must be >= 0");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (a->dtype) {
     case MFX_F32: return dispatch_typed<float, OP>(*a, s);
     case MFX_BF16: return dispatch_typed<bf16, OP>(*a, s);
-    default: return fail(MFX_E_UNSUPPORTED, "dtype must be f32 or bf16");
+    case MFX_F16: return dispatch_typed<_Float16, OP>(*a, s);
+    default: return fail(MFX_E_UNSUPPORTED, "dtype must be f32, bf16 or f16");
   }
 }
 

@@ -329,7 +329,11 @@ BwdPlan plan_bwd(const mfx_norm_bwd_args& a) {
   const bool aligned = a.n % VEC == 0 && a.x_row_stride % VEC == 0 && a.dy_row_stride % VEC == 0 &&
                        a.dx_row_stride % VEC == 0 && (uintptr_t)a.x % 16 == 0 &&
                        (uintptr_t)a.dy % 16 == 0 && (uintptr_t)a.dx % 16 == 0 &&
-                       (!a.gamma || (uintptr_t)a.gamma % palign == 0);
+                       (!a.gamma || (uintptr_t)a.gamma % palign == 0) &&
+                       // Vector kernels read gamma stored as f32 or as bf16
+                       // (f16 rows: f32 or f16).
+                       (!a.gamma || a.param_dtype == MFX_F32 ||
+                        a.param_dtype == (a.dtype == MFX_F16 ? MFX_F16 : MFX_BF16));
   const int64_t nvec = a.n / VEC;
   (void)es;
   // Register budget: at most 16 fp32 values per lane per row array.
@@ -391,9 +395,10 @@ const char* validate(const mfx_norm_bwd_args* a) {
   if (a->rows > 0 && (!a->x || !a->dy || !a->dx)) return "x, dy and dx must be non-null";
   if (a->x_row_stride < a->n || a->dy_row_stride < a->n || a->dx_row_stride < a->n)
     return "row strides must be >= n";
-  if (a->dtype != MFX_F32 && a->dtype != MFX_BF16) return "dtype must be f32 or bf16";
-  if ((a->gamma || a->dgamma || a->dbeta) && a->param_dtype != MFX_F32 && a->param_dtype != MFX_BF16)
-    return "param_dtype must be f32 or bf16";
+  if (a->dtype != MFX_F32 && a->dtype != MFX_BF16 && a->dtype != MFX_F16) return "dtype must be f32, bf16 or f16";
+  if ((a->gamma || a->dgamma || a->dbeta) && a->param_dtype != MFX_F32 && a->param_dtype != MFX_BF16 &&
+      a->param_dtype != MFX_F16)
+    return "param_dtype must be f32, bf16 or f16";
   if (!(a->eps >= 0.f)) return "eps must be >= 0";
   return nullptr;
 }
@@ -431,12 +436,15 @@ int mfx_layer_norm_bwd(const mfx_norm_bwd_args* args, void* stream) {
   if (a.rows == 0) {
     // Empty batch: the parameter gradients are empty sums (pass 2 with G = 0).
   } else if (p.vector) {
-    const bool pbf = a.param_dtype == MFX_BF16 && a.gamma;
+    const bool p16 = a.param_dtype != MFX_F32 && a.gamma;  // the row type's 16-bit kind (plan_bwd)
     if (a.dtype == MFX_F32) {
-      if (pbf) dispatch_rows_bwd<float, bf16>(a, p, partial, s);
+      if (p16) dispatch_rows_bwd<float, bf16>(a, p, partial, s);
       else dispatch_rows_bwd<float, float>(a, p, partial, s);
+    } else if (a.dtype == MFX_F16) {
+      if (p16) dispatch_rows_bwd<_Float16, _Float16>(a, p, partial, s);
+      else dispatch_rows_bwd<_Float16, float>(a, p, partial, s);
     } else {
-      if (pbf) dispatch_rows_bwd<bf16, bf16>(a, p, partial, s);
+      if (p16) dispatch_rows_bwd<bf16, bf16>(a, p, partial, s);
       else dispatch_rows_bwd<bf16, float>(a, p, partial, s);
     }
     if (int rc = launch_status("ln_bwd_rows")) return rc;
@@ -445,6 +453,11 @@ int mfx_layer_norm_bwd(const mfx_norm_bwd_args* args, void* stream) {
       hipLaunchKernelGGL((ln_bwd_rows_looped<float>), dim3((unsigned)p.groups), dim3(kBlock), 0, s,
                          static_cast<const float*>(a.x), static_cast<const float*>(a.dy),
                          static_cast<float*>(a.dx), a.gamma, a.param_dtype, partial, a.rows, a.n,
+                         a.x_row_stride, a.dy_row_stride, a.dx_row_stride, a.eps);
+    else if (a.dtype == MFX_F16)
+      hipLaunchKernelGGL((ln_bwd_rows_looped<_Float16>), dim3((unsigned)p.groups), dim3(kBlock), 0, s,
+                         static_cast<const _Float16*>(a.x), static_cast<const _Float16*>(a.dy),
+                         static_cast<_Float16*>(a.dx), a.gamma, a.param_dtype, partial, a.rows, a.n,
                          a.x_row_stride, a.dy_row_stride, a.dx_row_stride, a.eps);
     else
       hipLaunchKernelGGL((ln_bwd_rows_looped<bf16>), dim3((unsigned)p.groups), dim3(kBlock), 0, s,
@@ -459,6 +472,9 @@ int mfx_layer_norm_bwd(const mfx_norm_bwd_args* args, void* stream) {
   if (a.param_dtype == MFX_F32)
     hipLaunchKernelGGL((ln_bwd_params<float>), dim3(blocks), dim3(64 * kParamWaves), 0, s, partial, G, a.n,
                        static_cast<float*>(a.dgamma), static_cast<float*>(a.dbeta));
+  else if (a.param_dtype == MFX_F16)
+    hipLaunchKernelGGL((ln_bwd_params<_Float16>), dim3(blocks), dim3(64 * kParamWaves), 0, s, partial, G, a.n,
+                       static_cast<_Float16*>(a.dgamma), static_cast<_Float16*>(a.dbeta));
   else
     hipLaunchKernelGGL((ln_bwd_params<bf16>), dim3(blocks), dim3(64 * kParamWaves), 0, s, partial, G, a.n,
                        static_cast<bf16*>(a.dgamma), static_cast<bf16*>(a.dbeta));

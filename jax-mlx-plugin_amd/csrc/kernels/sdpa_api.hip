@@ -38,7 +38,8 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
     return fail(MFX_E_UNSUPPORTED, "problem too large for one launch");
   if (a->q_strides[3] != 1 || a->k_strides[3] != 1 || a->v_strides[3] != 1 || a->o_strides[3] != 1)
     return fail(MFX_E_INVALID, "feature (last) strides must be 1");
-  if (a->dtype != MFX_F32 && a->dtype != MFX_BF16) return fail(MFX_E_UNSUPPORTED, "dtype must be f32 or bf16");
+  if (a->dtype != MFX_F32 && a->dtype != MFX_BF16 && a->dtype != MFX_F16)
+    return fail(MFX_E_UNSUPPORTED, "dtype must be f32, bf16 or f16");
   if (a->mask && a->mask_dtype != MFX_F32 && a->mask_dtype != MFX_BF16 && a->mask_dtype != MFX_F16)
     return fail(MFX_E_UNSUPPORTED, "mask dtype must be f32, bf16 or f16");
   if (!std::isfinite(a->scale)) return fail(MFX_E_INVALID, "scale must be finite");
@@ -118,7 +119,9 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
 
 const char* kind_name(const Plan& pl) {
   switch (pl.kind) {
-    case Kind::kFlashBf16: return pl.p.D == 128 ? "flash_bf16_d128" : "flash_bf16_d64";
+    case Kind::kFlashBf16:
+      if (pl.p.dtype == MFX_F16) return pl.p.D == 128 ? "flash_f16_d128" : "flash_f16_d64";
+      return pl.p.D == 128 ? "flash_bf16_d128" : "flash_bf16_d64";
     case Kind::kFlashF32:
       if (flash_f32_use_split(pl.p)) return pl.p.D == 128 ? "flash_f32_split_d128" : "flash_f32_split_d64";
       return pl.p.D == 128 ? "flash_f32_d128" : "flash_f32_d64";

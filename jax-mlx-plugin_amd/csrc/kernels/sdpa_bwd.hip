@@ -13,11 +13,11 @@
 // group's query heads) and dQ per query row, so no output is accumulated by
 // two workgroups and the result is deterministic.
 //
-// The shape-general kernels here take any head size up to 256, f32 or bf16,
-// and every mask; one wavefront owns one output row and walks the other axis
-// in chunks of 64 (one score per lane), then accumulates its row with lanes
-// over features.  They are correct, not fast: bf16 with head size 64 / 128
-// runs on the matrix-core kernels (sdpa_bwd_mfma.hip).
+// The shape-general kernels here take any head size up to 256, f32, bf16 or
+// f16, and every mask; one wavefront owns one output row and walks the other
+// axis in chunks of 64 (one score per lane), then accumulates its row with
+// lanes over features.  They are correct, not fast: bf16 and f16 with head
+// size 64 / 128 run on the matrix-core kernels (sdpa_bwd_mfma.hip).
 #include <cmath>
 
 #include "sdpa_common.h"
@@ -199,7 +199,8 @@ int make_bwd_plan(const mfx_sdpa_bwd_args* a, BwdPlan& out) {
                           a->dq_strides, a->dk_strides, a->dv_strides, nullptr};
   for (int i = 0; st[i]; ++i)
     if (st[i][3] != 1) return fail(MFX_E_INVALID, "feature (last) strides must be 1");
-  if (a->dtype != MFX_F32 && a->dtype != MFX_BF16) return fail(MFX_E_UNSUPPORTED, "dtype must be f32 or bf16");
+  if (a->dtype != MFX_F32 && a->dtype != MFX_BF16 && a->dtype != MFX_F16)
+    return fail(MFX_E_UNSUPPORTED, "dtype must be f32, bf16 or f16");
   if (a->mask && a->mask_dtype != MFX_F32 && a->mask_dtype != MFX_BF16 && a->mask_dtype != MFX_F16)
     return fail(MFX_E_UNSUPPORTED, "mask dtype must be f32, bf16 or f16");
   if (!std::isfinite(a->scale)) return fail(MFX_E_INVALID, "scale must be finite");
@@ -309,6 +310,7 @@ const char* mfx_sdpa_bwd_kernel_name(const mfx_sdpa_bwd_args* args) {
   mfx::BwdPlan pl;
   if (mfx::make_bwd_plan(args, pl) != MFX_OK) return nullptr;
   if (!pl.mfma) return "generic";
+  if (pl.p.dtype == MFX_F16) return pl.p.D == 128 ? "mfma_f16_d128" : "mfma_f16_d64";
   return pl.p.D == 128 ? "mfma_bf16_d128" : "mfma_bf16_d64";
 }
 
@@ -350,6 +352,8 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
   const unsigned dblocks = (unsigned)((rows + 3) / 4);
   if (p.dtype == MFX_BF16)
     hipLaunchKernelGGL((bwd_delta_kernel<bf16>), dim3(dblocks), dim3(256), 0, s, p, delta);
+  else if (p.dtype == MFX_F16)
+    hipLaunchKernelGGL((bwd_delta_kernel<_Float16>), dim3(dblocks), dim3(256), 0, s, p, delta);
   else
     hipLaunchKernelGGL((bwd_delta_kernel<float>), dim3(dblocks), dim3(256), 0, s, p, delta);
   if ((rc = launch_status("bwd_delta_kernel")) != MFX_OK) return rc;
@@ -357,6 +361,9 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
   if (p.dtype == MFX_BF16) {
     hipLaunchKernelGGL((bwd_dkdv_generic<bf16>), dim3(kv_rows), dim3(64), 0, s, p);
     hipLaunchKernelGGL((bwd_dq_generic<bf16>), dim3((unsigned)rows), dim3(64), 0, s, p);
+  } else if (p.dtype == MFX_F16) {
+    hipLaunchKernelGGL((bwd_dkdv_generic<_Float16>), dim3(kv_rows), dim3(64), 0, s, p);
+    hipLaunchKernelGGL((bwd_dq_generic<_Float16>), dim3((unsigned)rows), dim3(64), 0, s, p);
   } else {
     hipLaunchKernelGGL((bwd_dkdv_generic<float>), dim3(kv_rows), dim3(64), 0, s, p);
     hipLaunchKernelGGL((bwd_dq_generic<float>), dim3((unsigned)rows), dim3(64), 0, s, p);

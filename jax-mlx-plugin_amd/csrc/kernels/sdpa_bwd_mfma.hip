@@ -1,5 +1,6 @@
-// Flash-attention backward on the matrix cores: bf16 inputs, head size 64 or
-// 128 (D == Dv), fp32 accumulation, v_mfma_f32_32x32x16_bf16 throughout.
+// Flash-attention backward on the matrix cores: bf16 or f16 inputs, head size
+// 64 or 128 (D == Dv), fp32 accumulation, v_mfma_f32_32x32x16_bf16 (f16: the
+// _f16 form) throughout.
 //
 // Two kernels, each owning its outputs (deterministic, no atomics):
 //
@@ -30,6 +31,7 @@
 // ragged tiles mask per element.
 #include <type_traits>
 
+#include "sdpa_elem.h"
 #include "sdpa_tiles.h"
 
 namespace mfx {
@@ -96,16 +98,16 @@ __device__ __forceinline__ void load_frags(const bf16* base, int64_t stride, int
 
 // Stores a transposed accumulator (rows d, lane column = one output row) as
 // bf16, 4 features per store, times `mul`.
-template <int D>
+template <int D, int E>
 __device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int half, float mul) {
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      bf16x4 w;
+      u16x4 w;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(acc[dt][g * 4 + e] * mul);
-      *reinterpret_cast<bf16x4*>(row + dt * 32 + g * 8 + half * 4) = w;
+      for (int e = 0; e < 4; ++e) w[e] = store_e<E>(acc[dt][g * 4 + e] * mul);
+      *reinterpret_cast<u16x4*>(row + dt * 32 + g * 8 + half * 4) = w;
     }
 }
 
@@ -125,7 +127,7 @@ __device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int hal
 constexpr int kKvPf = 2;   // operand reads issued ahead of their MFMAs
 constexpr int kKvStages = 3;
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, int E>
 __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   constexpr int TILE = kTile * D;    // elements of one Q or dO tile
   constexpr int TB = TILE * 2;       // its bytes
@@ -249,14 +251,14 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
       constexpr int ahead = 2 * (kKvPf < NK - 1 - j ? kKvPf : NK - 1 - j);
       lgkm_tie<ahead + 1>(qr[j]);
       if constexpr (j == 0)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qr[j], kf[j], f32x16{}, 0, 0, 0);
+        s = mfma16<E>(qr[j], kf[j], f32x16{});
       else
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qr[j], kf[j], s, 0, 0, 0);
+        s = mfma16<E>(qr[j], kf[j], s);
       lgkm_tie<ahead>(gr[j]);
       if constexpr (j == 0)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gr[j], vf[j], f32x16{}, 0, 0, 0);
+        dp = mfma16<E>(gr[j], vf[j], f32x16{});
       else
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(gr[j], vf[j], dp, 0, 0, 0);
+        dp = mfma16<E>(gr[j], vf[j], dp);
       fence();
     });
   };
@@ -310,9 +312,9 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(tr[j][0], tr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
       if constexpr ((j & 1) == 0)
-        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pd[PM][0][ks]), dv[dt], 0, 0, 0);
+        dv[dt] = mfma16<E>(a, __builtin_bit_cast(bf16x8, pd[PM][0][ks]), dv[dt]);
       else
-        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pd[PM][1][ks]), dk[dt], 0, 0, 0);
+        dk[dt] = mfma16<E>(a, __builtin_bit_cast(bf16x8, pd[PM][1][ks]), dk[dt]);
       if constexpr (VAL) {
         // Entry pairs (2k, 2k+1) of block (ST, MT), 8 over the 2*NT MFMAs.
 #pragma unroll
@@ -338,9 +340,7 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
             }
             ds[u] = pr[u] * (dv2[u] - dq4[r][e]);
           }
-          const bf16x2 wp = {static_cast<bf16>(pr[0]), static_cast<bf16>(pr[1])};
-          const bf16x2 wd = {static_cast<bf16>(ds[0]), static_cast<bf16>(ds[1])};
-          const uint32_t up = __builtin_bit_cast(uint32_t, wp), ud = __builtin_bit_cast(uint32_t, wd);
+          const uint32_t up = pack2<E>(pr[0], pr[1]), ud = pack2<E>(ds[0], ds[1]);
           asm volatile("" ::"v"(up), "v"(ud));
           pd[MT][0][k >> 2][k & 3] = up;
           pd[MT][1][k >> 2][k & 3] = ud;
@@ -404,8 +404,8 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   if (key < Tk) {
     bf16* dko = static_cast<bf16*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + (int64_t)key * p.dks[2];
     bf16* dvo = static_cast<bf16*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + (int64_t)key * p.dvs[2];
-    store_rowT<D>(dko, dk, half, p.scale);
-    store_rowT<D>(dvo, dv, half, 1.f);
+    store_rowT<D, E>(dko, dk, half, p.scale);
+    store_rowT<D, E>(dvo, dv, half, 1.f);
   }
 }
 
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
 // fragment pairs, transposed K fragment pairs).
 constexpr int kDqPf = 2;
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, int E>
 __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
   constexpr int TILE = kTile * D;  // elements of one K or V tile
   constexpr int TB = TILE * 2;     // its bytes
@@ -471,12 +471,24 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
     load_frags<D>(static_cast<const bf16*>(p.o) + b * p.os[0] + h * p.os[1], p.os[2], qi, Tq, half, of);
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
+    for (int kk = 0; kk < D / 16; ++kk) {
+      if constexpr (E == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        a0 = fmaf(static_cast<float>(gf[kk][e]), static_cast<float>(of[kk][e]), a0);
-        a1 = fmaf(static_cast<float>(gf[kk][e + 1]), static_cast<float>(of[kk][e + 1]), a1);
+        for (int e = 0; e < 8; e += 2) {
+          a0 = fmaf(elem_f32<E>(gf[kk][e]), elem_f32<E>(of[kk][e]), a0);
+          a1 = fmaf(elem_f32<E>(gf[kk][e + 1]), elem_f32<E>(of[kk][e + 1]), a1);
+        }
+      } else {
+        float gv[8], ov[8];
+        frag_f32_f16(gf[kk], gv);
+        frag_f32_f16(of[kk], ov);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          a0 = fmaf(gv[e], ov[e], a0);
+          a1 = fmaf(gv[e + 1], ov[e + 1], a1);
+        }
       }
+    }
     dl = a0 + a1;
     dl += __shfl_xor(dl, 32, 64);
   }
@@ -536,17 +548,18 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
       constexpr int ahead = 2 * (kDqPf < NK - 1 - j ? kDqPf : NK - 1 - j);
       lgkm_tie<ahead + 1>(kf[j]);
       if constexpr (j == 0)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], f32x16{}, 0, 0, 0);
+        s = mfma16<E>(kf[j], qf[j], f32x16{});
       else
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], s, 0, 0, 0);
+        s = mfma16<E>(kf[j], qf[j], s);
       lgkm_tie<ahead>(vf[j]);
       if constexpr (j == 0)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j], gf[j], f32x16{}, 0, 0, 0);
+        dp = mfma16<E>(vf[j], gf[j], f32x16{});
       else
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j], gf[j], dp, 0, 0, 0);
+        dp = mfma16<E>(vf[j], gf[j], dp);
       fence();
     });
     bf16x8 db[2];
+    float dsv[16];  // f16: dS before its rounding, packed by pairs below
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int key = kb + MT * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
@@ -561,7 +574,17 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
       if constexpr (EDGE) {
         if (key >= Tk || (CAUSAL && key > qi)) pr = 0.f;
       }
-      db[i >> 3][i & 7] = static_cast<bf16>(pr * (dp[i] - dl));
+      if constexpr (E == 0) db[i >> 3][i & 7] = f32_elem<E>(pr * (dp[i] - dl));
+      else dsv[i] = pr * (dp[i] - dl);
+    }
+    if constexpr (E != 0) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        float t[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = dsv[h2 * 8 + e];
+        db[h2] = f32_frag_f16(t);
+      }
     }
     // dQ MFMA j: d-block j % (D/32), 16-key step j / (D/32) of this block.
     s16x4 tr[NT][2];
@@ -580,7 +603,7 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
       lgkm_tie<2 * (kDqPf < NT - 1 - j ? kDqPf : NT - 1 - j)>(tr[j][0], tr[j][1]);
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(tr[j][0], tr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
-      dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db[ks], dq[dt], 0, 0, 0);
+      dq[dt] = mfma16<E>(a, db[ks], dq[dt]);
       fence();
     });
   };
@@ -616,25 +639,25 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
 
   if (qi < Tq) {
     bf16* dqo = static_cast<bf16*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + (int64_t)qi * p.dqs[2];
-    store_rowT<D>(dqo, dq, half, p.scale);
+    store_rowT<D, E>(dqo, dq, half, p.scale);
   }
 }
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, int E>
 int launch_t(const SdpaBwdParams& p, hipStream_t s) {
   const int64_t q_blocks = (int64_t)p.B * p.Hq * ((p.Tq + kRows - 1) / kRows);
-  hipLaunchKernelGGL((bwd_dq_mfma<D, CAUSAL, MASK>), dim3((unsigned)q_blocks), dim3(kNT), 0, s, p);
+  hipLaunchKernelGGL((bwd_dq_mfma<D, CAUSAL, MASK, E>), dim3((unsigned)q_blocks), dim3(kNT), 0, s, p);
   if (int rc = launch_status("bwd_dq_mfma")) return rc;
   const int64_t kv_blocks = (int64_t)p.B * p.Hkv * ((p.Tk + kRows - 1) / kRows);
-  hipLaunchKernelGGL((bwd_dkdv_mfma<D, CAUSAL, MASK>), dim3((unsigned)kv_blocks), dim3(kNT), 0, s, p);
+  hipLaunchKernelGGL((bwd_dkdv_mfma<D, CAUSAL, MASK, E>), dim3((unsigned)kv_blocks), dim3(kNT), 0, s, p);
   return launch_status("bwd_dkdv_mfma");
 }
 
-template <int D>
+template <int D, int E>
 int launch_d(const SdpaBwdParams& p, hipStream_t s) {
   const bool m = p.mask != nullptr;
-  if (p.causal) return m ? launch_t<D, true, true>(p, s) : launch_t<D, true, false>(p, s);
-  return m ? launch_t<D, false, true>(p, s) : launch_t<D, false, false>(p, s);
+  if (p.causal) return m ? launch_t<D, true, true, E>(p, s) : launch_t<D, true, false, E>(p, s);
+  return m ? launch_t<D, false, true, E>(p, s) : launch_t<D, false, false, E>(p, s);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -642,7 +665,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 }  // namespace
 
 bool bwd_mfma_supports(const SdpaBwdParams& p) {
-  if (p.dtype != MFX_BF16) return false;
+  if (p.dtype != MFX_BF16 && p.dtype != MFX_F16) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (!(p.scale_log2 > 0.f)) return false;
   // p.o is null until launch when O is recomputed (then it is the
@@ -671,8 +694,8 @@ bool bwd_mfma_supports(const SdpaBwdParams& p) {
 }
 
 int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s) {
-  if (p.D == 128) return launch_d<128>(p, s);
-  return launch_d<64>(p, s);
+  if (p.dtype == MFX_F16) return p.D == 128 ? launch_d<128, 1>(p, s) : launch_d<64, 1>(p, s);
+  return p.D == 128 ? launch_d<128, 0>(p, s) : launch_d<64, 0>(p, s);
 }
 
 }  // namespace mfx

@@ -39,6 +39,18 @@ __device__ __forceinline__ void unpack<bf16>(const u32x4& w, float* out) {
   }
 }
 template <>
+__device__ __forceinline__ void unpack<_Float16>(const u32x4& w, float* out) {
+  // Halves taken with integer shifts: a bit_cast of each dword to a 2 x f16
+  // vector compiles (f16 -> f32 folded into v_fma_mix) to products that all
+  // read the first dword.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t x = w[i];
+    out[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)(x & 0xffffu)));
+    out[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)(x >> 16)));
+  }
+}
+template <>
 __device__ __forceinline__ void unpack<float>(const u32x4& w, float* out) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(w[i]);
@@ -320,11 +332,11 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 }  // namespace
 
 bool decode_supports(const SdpaParams& p) {
-  if (p.dtype != MFX_BF16 && p.dtype != MFX_F32) return false;
+  if (p.dtype != MFX_BF16 && p.dtype != MFX_F16 && p.dtype != MFX_F32) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (p.group * p.Tq > 8) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v)) return false;
-  const int e = p.dtype == MFX_BF16 ? 8 : 4;
+  const int e = p.dtype == MFX_F32 ? 4 : 8;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % e || p.ks[i] % e || p.vs[i] % e) return false;
   return true;
@@ -334,6 +346,8 @@ int launch_decode_combine(const SdpaParams& p, hipStream_t s) {
   const unsigned blocks = (unsigned)(((int64_t)p.B * p.Hq * p.Tq + 3) / 4);
   if (p.dtype == MFX_BF16)
     hipLaunchKernelGGL((decode_combine_kernel<bf16>), dim3(blocks), dim3(256), 0, s, p);
+  else if (p.dtype == MFX_F16)
+    hipLaunchKernelGGL((decode_combine_kernel<_Float16>), dim3(blocks), dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((decode_combine_kernel<float>), dim3(blocks), dim3(256), 0, s, p);
   return launch_status("decode_combine_kernel");
@@ -341,6 +355,7 @@ int launch_decode_combine(const SdpaParams& p, hipStream_t s) {
 
 int launch_decode(const SdpaParams& p, hipStream_t s) {
   if (p.dtype == MFX_BF16) return p.D == 128 ? launch_d<bf16, 128>(p, s) : launch_d<bf16, 64>(p, s);
+  if (p.dtype == MFX_F16) return p.D == 128 ? launch_d<_Float16, 128>(p, s) : launch_d<_Float16, 64>(p, s);
   return p.D == 128 ? launch_d<float, 128>(p, s) : launch_d<float, 64>(p, s);
 }
 

@@ -38,6 +38,7 @@
 // used, exactly as the unfused graph rounds the RMSNorm output.
 #include <type_traits>
 
+#include "sdpa_elem.h"
 #include "sdpa_tiles.h"
 
 namespace mfx {
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(SdpaParams p) {
 // First element of wavefront w's range of the concatenated tile lists.
 __device__ __forceinline__ int64_t range_start(int w, int64_t T, int W) { return (int64_t)w * T / W; }
 
-template <int D, int MT, bool MB, bool CAUSAL>
+template <int D, int MT, bool MB, bool CAUSAL, int E>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   constexpr bool MASK = MT != 0;
   using Loader = tiles::TileLoader<D, kDN, 1>;
@@ -442,7 +443,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         for (int i = 0; i < 16; ++i) sc[mt][i] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk)
-          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk], qf[kk], sc[mt], 0, 0, 0);
+          sc[mt] = mfma16<E>(ka[kk], qf[kk], sc[mt]);
       }
       // V^T operand reads (transposing), issued now so that their latency
       // overlaps the softmax; inline asm for the same reason as the K reads.
@@ -489,22 +490,39 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       }
       const float nbase = b_run == -INFINITY ? 0.f : -b_run;
       bf16x8 pb[kKS];
+      if constexpr (E == 0) {
 #pragma unroll
-      for (int mt = 0; mt < kMT; ++mt)
+        for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(__builtin_amdgcn_exp2f(sc[mt][i] + nbase));
-      {
-        const bf16x2 one = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
+          for (int i = 0; i < 16; ++i)
+            pb[mt * 2 + (i >> 3)][i & 7] = f32_elem<E>(__builtin_amdgcn_exp2f(sc[mt][i] + nbase));
         float l0 = 0.f, l1 = 0.f;
 #pragma unroll
         for (int j = 0; j < kKS; ++j) {
           const bf16x8 wv = pb[j];
-          l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[0], wv[1]}, one, l0, false);
-          l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[2], wv[3]}, one, l1, false);
-          l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[4], wv[5]}, one, l0, false);
-          l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{wv[6], wv[7]}, one, l1, false);
+          l0 = dot2_at<E>(wv, 0, l0);
+          l1 = dot2_at<E>(wv, 2, l1);
+          l0 = dot2_at<E>(wv, 4, l0);
+          l1 = dot2_at<E>(wv, 6, l1);
         }
+        l_run += l0 + l1;
+      } else {
+        // f16: pairs packed into dwords first (per-element inserts and dot2
+        // operands compile to wrong row sums for f16).
+        u32x4 pw[kKS];
+        float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            const uint32_t w = pack2<E>(__builtin_amdgcn_exp2f(sc[mt][i] + nbase),
+                                        __builtin_amdgcn_exp2f(sc[mt][i + 1] + nbase));
+            pw[mt * 2 + (i >> 3)][(i & 7) >> 1] = w;
+            if ((i & 2) == 0) l0 = dot2<E>(w, l0);
+            else l1 = dot2<E>(w, l1);
+          }
+#pragma unroll
+        for (int j = 0; j < kKS; ++j) pb[j] = __builtin_bit_cast(bf16x8, pw[j]);
         l_run += l0 + l1;
       }
       lgkm_wait_tied(vr);
@@ -514,7 +532,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         for (int ks = 0; ks < kKS; ++ks) {
           const bf16x8 a =
               __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[dt][ks][0], vr[dt][ks][1], 0, 1, 2, 3, 4, 5, 6, 7));
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
+          o[dt] = mfma16<E>(a, pb[ks], o[dt]);
         }
     };
 
@@ -529,7 +547,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
       if (!qvalid) qf[kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-    if (qnorm) {
+    if (qnorm && E == 0) {
       float ss = 0.f;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk)
@@ -548,6 +566,28 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
           const float wv = wq ? static_cast<float>(wf[kk][e2]) : 1.f;
           qf[kk][e2] = static_cast<bf16>(static_cast<float>(qf[kk][e2]) * inv * wv);
         }
+    } else if (qnorm) {
+      // f16: whole fragments converted (see frag_f32_f16).
+      float ss = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+        float x[8];
+        frag_f32_f16(qf[kk], x);
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) ss += x[e2] * x[e2];
+      }
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+        float x[8], w[8];
+        frag_f32_f16(qf[kk], x);
+        if (wq) frag_f32_f16(wf[kk], w);
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) x[e2] = x[e2] * inv * (wq ? w[e2] : 1.f);
+        qf[kk] = f32_frag_f16(x);
+      }
     }
     for (int i = 0; i < ntl; i += 3) {
       body(i, k0, v0, k2, v2);
@@ -729,42 +769,44 @@ bool mask_rows_shared(const SdpaParams& p) {
   return (p.ms[1] == 0 || p.group == 1) && (p.ms[2] == 0 || p.Tq == 1);
 }
 
-template <int D, int MT, bool MB, bool CAUSAL>
+template <int D, int MT, bool MB, bool CAUSAL, int E>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   hipLaunchKernelGGL((decode_tiles_kernel<MT, CAUSAL>), dim3((unsigned)(p.B * p.Hkv)), dim3(256), 0, s, p);
   int rc = launch_status("decode_tiles_kernel");
   if (rc != MFX_OK) return rc;
-  hipLaunchKernelGGL((decode_mfma_kernel<D, MT, MB, CAUSAL>), dim3((unsigned)p.num_splits), dim3(64), 0, s, p);
+  hipLaunchKernelGGL((decode_mfma_kernel<D, MT, MB, CAUSAL, E>), dim3((unsigned)p.num_splits), dim3(64), 0, s, p);
   if ((rc = launch_status("decode_mfma_kernel")) != MFX_OK) return rc;
   const unsigned blocks = (unsigned)(((int64_t)p.B * p.Hq * p.Tq + 3) / 4);
-  hipLaunchKernelGGL((decode_bal_combine_kernel<bf16, D>), dim3(blocks), dim3(256), 0, s, p);
+  using OT = std::conditional_t<E == 0, bf16, _Float16>;
+  hipLaunchKernelGGL((decode_bal_combine_kernel<OT, D>), dim3(blocks), dim3(256), 0, s, p);
   return launch_status("decode_bal_combine_kernel");
 }
 
-template <int D, int MT, bool CAUSAL>
+template <int D, int MT, bool CAUSAL, int E>
 int launch_m(const SdpaParams& p, hipStream_t s) {
-  if constexpr (MT == 0) return launch_t<D, 0, true, CAUSAL>(p, s);
-  else return mask_rows_shared(p) ? launch_t<D, MT, true, CAUSAL>(p, s) : launch_t<D, MT, false, CAUSAL>(p, s);
+  if constexpr (MT == 0) return launch_t<D, 0, true, CAUSAL, E>(p, s);
+  else
+    return mask_rows_shared(p) ? launch_t<D, MT, true, CAUSAL, E>(p, s) : launch_t<D, MT, false, CAUSAL, E>(p, s);
+}
+
+template <int D, bool CAUSAL, int E>
+int launch_c(const SdpaParams& p, hipStream_t s) {
+  switch (p.mask ? mask_code(p.mask_dtype) : 0) {
+    case 1: return launch_m<D, 1, CAUSAL, E>(p, s);
+    case 2: return launch_m<D, 2, CAUSAL, E>(p, s);
+    case 3: return launch_m<D, 3, CAUSAL, E>(p, s);
+    default: return launch_m<D, 0, CAUSAL, E>(p, s);
+  }
+}
+
+template <int D, int E>
+int launch_e(const SdpaParams& p, hipStream_t s) {
+  return p.causal ? launch_c<D, true, E>(p, s) : launch_c<D, false, E>(p, s);
 }
 
 template <int D>
 int launch_d(const SdpaParams& p, hipStream_t s) {
-  const bool m = p.mask != nullptr;
-  const int mt = m ? mask_code(p.mask_dtype) : 0;
-  if (p.causal) {
-    switch (mt) {
-      case 1: return launch_m<D, 1, true>(p, s);
-      case 2: return launch_m<D, 2, true>(p, s);
-      case 3: return launch_m<D, 3, true>(p, s);
-      default: return launch_m<D, 0, true>(p, s);
-    }
-  }
-  switch (mt) {
-    case 1: return launch_m<D, 1, false>(p, s);
-    case 2: return launch_m<D, 2, false>(p, s);
-    case 3: return launch_m<D, 3, false>(p, s);
-    default: return launch_m<D, 0, false>(p, s);
-  }
+  return p.dtype == MFX_F16 ? launch_e<D, 1>(p, s) : launch_e<D, 0>(p, s);
 }
 
 template <int D>
@@ -778,7 +820,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 }  // namespace
 
 bool decode_mfma_supports(const SdpaParams& p) {
-  if (p.dtype != MFX_BF16) return false;
+  if (p.dtype != MFX_BF16 && p.dtype != MFX_F16) return false;
   if (!(p.scale_log2 > 0.f)) return false;
   if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
   if (p.group * p.Tq > 32) return false;

@@ -33,6 +33,7 @@
 // first, which balances the causal triangle across the CUs.
 #include <type_traits>
 
+#include "sdpa_elem.h"
 #include "sdpa_tiles.h"
 
 namespace mfx {
@@ -52,7 +53,7 @@ using tiles::wait_dma;
 template <int D>
 using TileLoader = tiles::TileLoader<D, kBN, kNT / 64>;
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, int E>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   __shared__ __attribute__((aligned(16))) bf16 k0[kBN * D];
   __shared__ __attribute__((aligned(16))) bf16 v0[kBN * D];
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
         const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kl[mt * 32 * D + k_off + ((kk * 2 + half) ^ k_sw) * 8]);
-        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[mt], 0, 0, 0);
+        s[mt] = mfma16<E>(a, qf[kk], s[mt]);
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -191,30 +192,44 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
         for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
     }
     const float nbase = b_run == -INFINITY ? 0.f : -b_run;
+    auto pexp = [&](int mt, int i) {
+      return MASK ? __builtin_amdgcn_exp2f(s[mt][i] + nbase) : __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
+    };
+    // P rounded to the element type and the row sum of exactly the rounded
+    // values the PV product consumes, two per instruction.
     bf16x8 pb[kKS];
+    float l0 = 0.f, l1 = 0.f;
+    if constexpr (E == 0) {
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
+      for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pv = MASK ? __builtin_amdgcn_exp2f(s[mt][i] + nbase)
-                              : __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
-        pb[mt * 2 + (i >> 3)][i & 7] = static_cast<bf16>(pv);
-      }
-    // Row sum of exactly the bf16 values the PV product consumes, two per
-    // instruction.
-    {
-      const bf16x2 one = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
-      float l0 = 0.f, l1 = 0.f;
+        for (int i = 0; i < 16; ++i) pb[mt * 2 + (i >> 3)][i & 7] = f32_elem<E>(pexp(mt, i));
 #pragma unroll
       for (int j = 0; j < kKS; ++j) {
         const bf16x8 w = pb[j];
-        l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[0], w[1]}, one, l0, false);
-        l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[2], w[3]}, one, l1, false);
-        l0 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[4], w[5]}, one, l0, false);
-        l1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w[6], w[7]}, one, l1, false);
+        l0 = dot2_at<E>(w, 0, l0);
+        l1 = dot2_at<E>(w, 2, l1);
+        l0 = dot2_at<E>(w, 4, l0);
+        l1 = dot2_at<E>(w, 6, l1);
       }
-      l_run += l0 + l1;
+    } else {
+      // f16: pairs packed into dwords first.  (Element inserts into the
+      // 16-bit vector followed by per-element dot2 operands compile to
+      // wrong row sums for f16: pairs built from one value twice.)
+      u32x4 pw[kKS];
+#pragma unroll
+      for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const uint32_t w = pack2<E>(pexp(mt, i), pexp(mt, i + 1));
+          pw[mt * 2 + (i >> 3)][(i & 7) >> 1] = w;
+          if ((i & 2) == 0) l0 = dot2<E>(w, l0);
+          else l1 = dot2<E>(w, l1);
+        }
+#pragma unroll
+      for (int j = 0; j < kKS; ++j) pb[j] = __builtin_bit_cast(bf16x8, pw[j]);
     }
+    l_run += l0 + l1;
     __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
@@ -227,7 +242,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (lds_s16x4_t*)(v_rows + 8 * D + ((dt * 4 + v_chunk) ^ v_sw8) * 8));
         const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[dt], 0, 0, 0);
+        o[dt] = mfma16<E>(a, pb[ks], o[dt]);
       }
   };
 
@@ -272,25 +287,25 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        bf16x4 w;
+        u16x4 w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(o[dt][g * 4 + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
+        for (int e = 0; e < 4; ++e) w[e] = store_e<E>(o[dt][g * 4 + e] * inv);
+        *reinterpret_cast<u16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
       }
   }
 }
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, int E>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   const int nmb = (p.Tq + kBM - 1) / kBM;
   const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
-  hipLaunchKernelGGL((flash_bf16_kernel<D, CAUSAL, MASK>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
+  hipLaunchKernelGGL((flash_bf16_kernel<D, CAUSAL, MASK, E>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
   return launch_status("flash_bf16_kernel");
 }
 
-template <int D>
+template <int D, int E>
 int launch_d(const SdpaParams& p, hipStream_t s) {
-  return p.causal ? launch_t<D, true, true>(p, s) : launch_t<D, false, true>(p, s);
+  return p.causal ? launch_t<D, true, true, E>(p, s) : launch_t<D, false, true, E>(p, s);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -298,7 +313,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 }  // namespace
 
 bool flash_bf16_supports(const SdpaParams& p) {
-  if (p.dtype != MFX_BF16) return false;
+  if (p.dtype != MFX_BF16 && p.dtype != MFX_F16) return false;
   if (!(p.scale_log2 > 0.f)) return false;  // the exp2 FMA folds a positive scale
   // K/V rows are read through one buffer resource per head spanning its Tk
   // rows, range-checked on 31-bit lane offsets: row strides of at least D
@@ -320,8 +335,8 @@ int launch_flash_bf16(const SdpaParams& p, hipStream_t s) {
   // rows, the software-pipelined kernel runs (sdpa_flash_bf16_pipe.hip);
   // this file's kernel serves masks with a query-row stride.
   if (!p.mask || p.ms[2] == 0) return launch_flash_bf16_pipe(p, s);
-  if (p.D == 128) return launch_d<128>(p, s);
-  return launch_d<64>(p, s);
+  if (p.dtype == MFX_F16) return p.D == 128 ? launch_d<128, 1>(p, s) : launch_d<64, 1>(p, s);
+  return p.D == 128 ? launch_d<128, 0>(p, s) : launch_d<64, 0>(p, s);
 }
 
 }  // namespace mfx

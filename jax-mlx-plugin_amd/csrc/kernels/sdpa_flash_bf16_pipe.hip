@@ -58,6 +58,7 @@
 // jax-mlx-plugin_amd/phase_budget.py turns them into the per-tile budget.
 #include <type_traits>
 
+#include "sdpa_elem.h"
 #include "sdpa_tiles.h"
 
 #if defined(MFX_PHASE_TIMERS)
@@ -134,9 +135,9 @@ constexpr int kPfV = 4;   // V read pairs issued ahead of their PV MFMA
 constexpr int kHeadGroup = 4;  // heads whose q-blocks an XCD issues together
 
 using tiles::kSlack;
-// Row-sum cap of one tile (32 keys per lane): a sum above it (or NaN) means a
-// score passed the base by more than log2(kSumCap / 32) = 11 > kSlack.
-constexpr float kSumCap = 65536.f;
+// Row-sum cap of one tile (32 keys per lane), kMaxP of the element type: a
+// sum above it (or NaN) means a score passed the base by more than
+// log2(kMaxP / 32) = 11 (bf16) or 10 (f16) > kSlack.
 using tiles::s16x4;
 using tiles::tile_swz;
 using tiles::wait_dma;
@@ -192,7 +193,7 @@ struct Loader {
 constexpr int wait_k(int j, int MS, int pf) { return pf < MS - 1 - j ? pf : MS - 1 - j; }
 constexpr int wait_v(int j, int MP, int pf) { return 2 * (pf < MP - 1 - j ? pf : MP - 1 - j); }
 
-template <int D, bool CAUSAL, int MT>
+template <int D, bool CAUSAL, int MT, int E>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   constexpr int TILE = kBN * D;     // elements of one K or V tile
   constexpr int TB = TILE * 2;      // its bytes
@@ -202,6 +203,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   // Operand reads ahead of their MFMA: 2, 4 and 6 measured alike on config
   // 3; a masked kernel keeps 2 for the registers its mask rows take.
   constexpr int PFK = MASK ? 2 : kPfK, PFV = MASK ? 2 : kPfV;
+  constexpr float kSumCap = kMaxP<E>;
   static_assert(MS % 8 == 0 || 8 % MS == 0, "interleave");
   __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 K1 V0 V1
   // Mask rows (raw score units) of the tiles in K stages 0 / 1 (MASK only):
@@ -393,16 +395,14 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   };
-  // exp2 of pair g of S (keys 2g, 2g+1 of the lane's 32) into P (bf16) and
-  // the row sum of exactly those bf16 values.
-  const bf16x2 one2 = {static_cast<bf16>(1.f), static_cast<bf16>(1.f)};
+  // exp2 of pair g of S (keys 2g, 2g+1 of the lane's 32) into P (element
+  // type E) and the row sum of exactly those rounded values.
   auto exp_pair = [&](f32x16 (&s)[2], int g, u32x4 (&dst)[2], float& acc) {
     const int mt = g >> 3, i = (g & 7) * 2;
     const float p0 = __builtin_amdgcn_exp2f(fmaf(s[mt][i], sl2, nbase));
     const float p1 = __builtin_amdgcn_exp2f(fmaf(s[mt][i + 1], sl2, nbase));
-    const bf16x2 w = {static_cast<bf16>(p0), static_cast<bf16>(p1)};
-    const uint32_t wu = __builtin_bit_cast(uint32_t, w);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(w, one2, acc, false);
+    const uint32_t wu = pack2<E>(p0, p1);
+    acc = dot2<E>(wu, acc);
     // Keeps the work in this MFMA's slot: without a use here the compiler
     // sinks it past the branches between the phases, behind the MFMAs.
     asm volatile("" ::"v"(wu), "v"(acc));
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) s[mt] = mask_seed(0, mt);
 #pragma unroll
-    for (int j = 0; j < MS; ++j) s[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], s[j & 1], 0, 0, 0);
+    for (int j = 0; j < MS; ++j) s[j & 1] = mfma16<E>(kr[j], qf[j >> 1], s[j & 1]);
   };
 
   // One tile t: K stage KS holds tile t+1, V stage VS tile t; sc = S(t)
@@ -491,10 +491,10 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       if constexpr (j + PFK < MS) rdk(std::integral_constant<int, j + PFK>{});
       lgkm_tie<wait_k(j, MS, PFK)>(kr[j]);
       if constexpr (j < 2) {
-        sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], j ? seed1 : seed0, 0, 0, 0);
+        sn[j & 1] = mfma16<E>(kr[j], qf[j >> 1], j ? seed1 : seed0);
         if constexpr (MASK && j == 0) seed1 = mask_seed((t + 1) & 1, 1);
       } else {
-        sn[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[j], qf[j >> 1], sn[j & 1], 0, 0, 0);
+        sn[j & 1] = mfma16<E>(kr[j], qf[j >> 1], sn[j & 1]);
       }
 #pragma unroll
       for (int g = 8 + j * 8 / MS; g < 8 + (j + 1) * 8 / MS; ++g) exp_pair(sc, g, pb, ls);
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
       const u32x4 pbk = ks < 2 ? pc[ks & 1] : pb[ks & 1];
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pbk), o[dt], 0, 0, 0);
+      o[dt] = mfma16<E>(a, __builtin_bit_cast(bf16x8, pbk), o[dt]);
 #pragma unroll
       for (int g = j * 8 / MP; g < (j + 1) * 8 / MP; ++g) exp_pair(sn, g, pn, lf);
       fence();
@@ -555,7 +555,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       const bf16x8 a =
           __builtin_bit_cast(bf16x8, __builtin_shufflevector(vr[j][0], vr[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
       const u32x4 pbk = ks < 2 ? pc[ks & 1] : pb[ks & 1];
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, pbk), o[dt], 0, 0, 0);
+      o[dt] = mfma16<E>(a, __builtin_bit_cast(bf16x8, pbk), o[dt]);
       fence();
     });
   };
@@ -638,48 +638,54 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        bf16x4 w;
+        u16x4 w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = static_cast<bf16>(o[dt][g * 4 + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
+        for (int e = 0; e < 4; ++e) w[e] = store_e<E>(o[dt][g * 4 + e] * inv);
+        *reinterpret_cast<u16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
       }
   }
   PHASE(fence(); ph.write(lane, id * kNW + wave, bh, mblk, N, nw, c_epi);)
 }
 
-template <int D, bool CAUSAL, int MT>
+template <int D, bool CAUSAL, int MT, int E>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   const int nmb = (p.Tq + kBM - 1) / kBM;
   const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
-  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, CAUSAL, MT>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
+  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, CAUSAL, MT, E>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
   return launch_status("flash_bf16_pipe_kernel");
 }
 
-template <int D, int MT>
+template <int D, int MT, int E>
 int launch_c(const SdpaParams& p, hipStream_t s) {
-  return p.causal ? launch_t<D, true, MT>(p, s) : launch_t<D, false, MT>(p, s);
+  return p.causal ? launch_t<D, true, MT, E>(p, s) : launch_t<D, false, MT, E>(p, s);
 }
 
-template <int D>
+template <int D, int E>
 int launch_m(const SdpaParams& p, hipStream_t s) {
-  if (!p.mask) return launch_c<D, 0>(p, s);
+  if (!p.mask) return launch_c<D, 0, E>(p, s);
 #if defined(MFX_PHASE_TIMERS)
   // The diagnostic build instruments the mask-free kernels only.
   return fail(MFX_E_UNSUPPORTED, "phase-timer build: masked attention is not instrumented");
 #else
-  if (p.mask_dtype == MFX_F32) return launch_c<D, 1>(p, s);
-  if (p.mask_dtype == MFX_BF16) return launch_c<D, 2>(p, s);
-  return launch_c<D, 3>(p, s);
+  if (p.mask_dtype == MFX_F32) return launch_c<D, 1, E>(p, s);
+  if (p.mask_dtype == MFX_BF16) return launch_c<D, 2, E>(p, s);
+  return launch_c<D, 3, E>(p, s);
 #endif
+}
+
+template <int E>
+int launch_d(const SdpaParams& p, hipStream_t s) {
+  if (p.D == 128) return launch_m<128, E>(p, s);
+  return launch_m<64, E>(p, s);
 }
 
 }  // namespace
 
 // Flash attention without an additive mask or with one that does not vary
-// along query rows, p.ms[2] == 0 (the caller checked flash_bf16_supports).
+// along query rows, p.ms[2] == 0 (the caller checked flash_bf16_supports);
+// q, k, v and out all bf16 or all f16 (p.dtype).
 int launch_flash_bf16_pipe(const SdpaParams& p, hipStream_t s) {
-  if (p.D == 128) return launch_m<128>(p, s);
-  return launch_m<64>(p, s);
+  return p.dtype == MFX_F16 ? launch_d<1>(p, s) : launch_d<0>(p, s);
 }
 
 }  // namespace mfx

@@ -1,5 +1,5 @@
 // Shape-general SDPA: any head size up to 256, any strides whose feature
-// stride is 1, f32 or bf16, causal / additive mask / GQA / fused q RMSNorm.
+// stride is 1, f32, bf16 or f16, causal / additive mask / GQA / fused q RMSNorm.
 // One wavefront per query row; keys stream in chunks of 64 (one score per
 // lane, online softmax per chunk), values accumulate with each lane owning
 // features lane, lane+64, ...  This kernel covers the shapes the MFMA and
@@ -100,6 +100,8 @@ int launch_generic(const SdpaParams& p, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * p.Hq * p.Tq;
   if (p.dtype == MFX_BF16)
     hipLaunchKernelGGL((generic_kernel<bf16>), dim3((unsigned)rows), dim3(64), 0, s, p);
+  else if (p.dtype == MFX_F16)
+    hipLaunchKernelGGL((generic_kernel<_Float16>), dim3((unsigned)rows), dim3(64), 0, s, p);
   else
     hipLaunchKernelGGL((generic_kernel<float>), dim3((unsigned)rows), dim3(64), 0, s, p);
   return launch_status("generic_kernel");

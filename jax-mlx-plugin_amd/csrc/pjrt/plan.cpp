@@ -969,9 +969,10 @@ class Planner {
     a.param_dtype = mfx_dtype(ty(dg).dtype);
     if (ty(dy).dtype != t.dtype || ty(dx).dtype != t.dtype || ty(gamma).dtype != ty(dg).dtype)
       throw ParseError("mlx_layer_norm_bwd: x / grad_out / dx and weight / dweight dtypes must match");
-    if (a.dtype != MFX_F32 && a.dtype != MFX_BF16) throw ParseError("mlx_layer_norm_bwd: x must be f32 or bf16");
-    if (a.param_dtype != MFX_F32 && a.param_dtype != MFX_BF16)
-      throw ParseError("mlx_layer_norm_bwd: weight must be f32 or bf16");
+    if (a.dtype != MFX_F32 && a.dtype != MFX_BF16 && a.dtype != MFX_F16)
+      throw ParseError("mlx_layer_norm_bwd: x must be f32, bf16 or f16");
+    if (a.param_dtype != MFX_F32 && a.param_dtype != MFX_BF16 && a.param_dtype != MFX_F16)
+      throw ParseError("mlx_layer_norm_bwd: weight must be f32, bf16 or f16");
     check_dense("norm bwd x", x, a.rows * a.n);
     check_dense("norm bwd dy", dy, a.rows * a.n);
     check_dense("norm bwd dx", dx, a.rows * a.n);
@@ -1049,7 +1050,8 @@ class Planner {
       if (ty(v).dtype != dt) throw ParseError("mlx_sdpa_bwd operands must share one dtype");
     for (int v : n.out)
       if (ty(v).dtype != dt) throw ParseError("mlx_sdpa_bwd results must have the operands' dtype");
-    if (a.dtype != MFX_F32 && a.dtype != MFX_BF16) throw ParseError("mlx_sdpa_bwd: dtype must be f32 or bf16");
+    if (a.dtype != MFX_F32 && a.dtype != MFX_BF16 && a.dtype != MFX_F16)
+      throw ParseError("mlx_sdpa_bwd: dtype must be f32, bf16 or f16");
     for (int i = 0; i < 4; ++i) check_dense("sdpa bwd operand", n.in[i], ty(n.in[i]).numel());
     for (int i = 0; i < 3; ++i) check_dense("sdpa bwd result", n.out[i], ty(n.out[i]).numel());
     mfx_sdpa_bwd_args probe = a;

@@ -34,6 +34,9 @@ namespace {
 
 bool op_is(const Node* n, const char* name) { return n && n->op == name; }
 
+// Element types the fused kernels read and write (fp32 arithmetic inside).
+bool kernel_float(DType t) { return t == DType::kF32 || t == DType::kBF16 || t == DType::kF16; }
+
 std::vector<int> use_counts(const Function& f) {
   std::vector<int> u(f.values.size(), 0);
   for (const Node& n : f.nodes)
@@ -408,9 +411,9 @@ int rewrite_norms(Ctx& c, RewriteStats& st) {
       x = xs;
     }
     if (c.ty(x).dtype != c.ty(out_v).dtype || c.ty(x).dims != c.ty(out_v).dims) continue;
-    if (c.ty(x).dtype != DType::kF32 && c.ty(x).dtype != DType::kBF16) continue;
+    if (!kernel_float(c.ty(x).dtype)) continue;
     for (int p : {gamma, beta})
-      if (p >= 0 && c.ty(p).dtype != DType::kF32 && c.ty(p).dtype != DType::kBF16) gamma = beta = -2;
+      if (p >= 0 && !kernel_float(c.ty(p).dtype)) gamma = beta = -2;
     if (gamma == -2) continue;
     Node fused;
     fused.op = m.rms ? "mfx.rms_norm" : "mfx.layer_norm";
@@ -479,8 +482,7 @@ int rewrite_softmax(Ctx& c, RewriteStats& st) {
     int x;
     if (!match_softmax(c, n.out[0], x)) continue;
     if (c.ty(x) != c.ty(n.out[0])) continue;
-    DType dt = c.ty(x).dtype;
-    if (dt != DType::kF32 && dt != DType::kBF16) continue;
+    if (!kernel_float(c.ty(x).dtype)) continue;
     Node fused;
     fused.op = "mfx.softmax";
     fused.in = {x};
@@ -525,8 +527,7 @@ int rewrite_log_softmax(Ctx& c, RewriteStats& st) {
     int x;
     if (!match_log_softmax(c, n.out[0], x)) continue;
     if (c.ty(x) != c.ty(n.out[0])) continue;
-    const DType dt = c.ty(x).dtype;
-    if (dt != DType::kF32 && dt != DType::kBF16) continue;
+    if (!kernel_float(c.ty(x).dtype)) continue;
     Node fused;
     fused.op = "mfx.log_softmax";
     fused.in = {x};
@@ -1139,11 +1140,11 @@ int rewrite_sdpa(Ctx& c, RewriteStats& st) {
     }
     if (mask_kind) {
       DType md = c.ty(mask_in).dtype;
-      if (mask_kind == 1 && md != DType::kF32 && md != DType::kBF16 && md != DType::kF16) continue;
+      if (mask_kind == 1 && !kernel_float(md)) continue;
     }
     DType qd = c.ty(qv.base).dtype, kd = c.ty(kv.base).dtype, vd = c.ty(vv.base).dtype;
     DType od = c.ty(out_v).dtype;
-    if (qd != kd || kd != vd || (qd != DType::kF32 && qd != DType::kBF16)) continue;
+    if (qd != kd || kd != vd || !kernel_float(qd)) continue;
     if (od != qd) {
       // f32 accumulate then convert: absorb a trailing convert to the input dtype.
       int u = single_user(c, out_v);

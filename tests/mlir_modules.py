@@ -33,7 +33,8 @@ def ty(shape, dt):
 
 def f32_lit(x: float, dt: str = "f32") -> str:
     if math.isinf(x):
-        bits = {"f32": 0xFF800000 if x < 0 else 0x7F800000, "bf16": 0xFF80 if x < 0 else 0x7F80}[dt]
+        bits = {"f32": 0xFF800000 if x < 0 else 0x7F800000, "bf16": 0xFF80 if x < 0 else 0x7F80,
+                "f16": 0xFC00 if x < 0 else 0x7C00}[dt]
         width = 8 if dt == "f32" else 4
         return f"0x{bits:0{width}X}"
     return f"{x:.8E}"

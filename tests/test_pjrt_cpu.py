@@ -434,6 +434,31 @@ def test_custom_calls(api):
     assert steps(d) == ["sdpa_bwd"] and d["plan"]["arena_bytes"] > 0  # recomputed O, lse, delta
 
 
+def test_f16_modules_fuse(api):
+    """f16 graphs take the same fused kernels as bf16 (the reference hands f16
+    to the same MLX fast ops, src/jax_mlx_pjrt.cpp:317-349): LayerNorm (var
+    and Flax forms), RMSNorm, softmax, log-softmax, SDPA (BHTD causal, the
+    jax.nn form with a bias, GQA decode with q RMSNorm) and both backward
+    custom calls."""
+    def ops(text):
+        return [n["op"] for n in fused(api.inspect(text))]
+
+    assert ops(M.layer_norm_module(dt="f16")) == ["mfx.layer_norm"]
+    assert ops(M.layer_norm_module(shape=(4, 64, 256), dt="f16", form="flax")) == ["mfx.layer_norm"]
+    assert ops(M.rms_norm_module(dt="f16")) == ["mfx.rms_norm"]
+    assert ops(M.rms_norm_module(dt="f16", upcast=True)) == ["mfx.rms_norm"]
+    assert ops(M.softmax_module(dt="f16")) == ["mfx.softmax"]
+    assert ops(M.log_softmax_module((6, 64), dt="f16")) == ["mfx.log_softmax"]
+    d = api.inspect(M.sdpa_bhtd_module(B=2, H=4, T=256, D=128, dt="f16", causal=True))
+    (n,) = fused(d)
+    assert n["op"] == "mfx.sdpa" and n["i:causal"] == [1] and steps(d) == ["sdpa"]
+    assert ops(M.dot_product_attention_module(B=2, T=64, N=8, K=2, H=64, dt="f16", is_causal=False,
+                                              bias=True)) == ["mfx.sdpa"]
+    assert ops(M.gqa_decode_module(B=2, S=512, dt="f16")) == ["mfx.sdpa"]
+    assert ops(M.custom_call_sdpa_bwd_module(dt="f16")) == ["mfx.sdpa_bwd"]
+    assert ops(M.custom_call_layer_norm_bwd_module(dt="f16")) == ["mfx.layer_norm_bwd"]
+
+
 def test_custom_call_sdpa_shape_mismatch(api):
     """mlx_sdpa checks k and v against q as mlx_sdpa_bwd does: a head size or
     sequence length that disagrees, or N not a multiple of K, is a compile

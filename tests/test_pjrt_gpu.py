@@ -43,7 +43,11 @@ def host_arg(a, dt):
     import torch
 
     t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
-    return t.bfloat16() if dt == "bf16" else t
+    return {"bf16": t.bfloat16, "f16": t.half}.get(dt, lambda: t)()
+
+
+def f16_round(a):
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float64)
 
 
 def run(client, text, arrays, dts):
@@ -555,7 +559,81 @@ def test_dense_epilogue_unaligned_weights_fall_back(client):
     assert np.abs(outs[0] - outs[1]).max() <= 1e-5
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
+# f16 through the same fused paths.  Bar: ||out - ref||_inf / ||ref||_inf
+# <= 5e-3 (f16's 11 significant bits; the kernel tests' f16 bar), against
+# the oracle on the f16-rounded inputs.
+F16_REL_TOL = 5e-3
+
+
+def test_f16_norms_through_pjrt(client, oracle):
+    rng = np.random.default_rng(91)
+    x = f16_round(rng.standard_normal((8, 128, 512)) * 2 + 0.5)
+    g = f16_round(1 + 0.1 * rng.standard_normal(512))
+    b = f16_round(0.1 * rng.standard_normal(512))
+    (y,) = run(client, M.layer_norm_module(dt="f16"), [x, g, b], ["f16"] * 3)
+    assert rel_inf(y, oracle.layer_norm(x, g, b, 1e-5)) <= F16_REL_TOL
+    (y,) = run(client, M.layer_norm_module(shape=(4, 64, 256), dt="f16", form="flax"),
+               [x[:4, :64, :256], g[:256], b[:256]], ["f16"] * 3)
+    assert rel_inf(y, oracle.layer_norm(x[:4, :64, :256], g[:256], b[:256], 1e-5)) <= F16_REL_TOL
+    xr = x[:2, :4, :128]
+    (y,) = run(client, M.rms_norm_module(dt="f16", upcast=True), [xr, g[:128]], ["f16", "f16"])
+    assert rel_inf(y, oracle.rms_norm(xr, g[:128], 1e-6)) <= F16_REL_TOL
+    xs = f16_round(rng.standard_normal((6, 64)) * 4)
+    (y,) = run(client, M.softmax_module(dt="f16"), [xs], ["f16"])
+    assert rel_inf(y, oracle.softmax(xs)) <= F16_REL_TOL
+    (y,) = run(client, M.log_softmax_module((6, 64), dt="f16"), [xs], ["f16"])
+    assert rel_inf(y, oracle.log_softmax(xs)) <= F16_REL_TOL
+
+
+def test_f16_attention_through_pjrt(client, oracle):
+    """Causal BHTD prefill, the jax.nn BTNH form with GQA and a bias, and
+    GQA decode with q RMSNorm over a length mask, all f16."""
+    rng = np.random.default_rng(92)
+    q, k, v = (f16_round(rng.standard_normal((1, 4, 256, 128))) for _ in range(3))
+    (o,) = run(client, M.sdpa_bhtd_module(B=1, H=4, T=256, D=128, dt="f16", causal=True), [q, k, v], ["f16"] * 3)
+    assert rel_inf(o, oracle.sdpa(q, k, v, 1 / math.sqrt(128), causal=True)) <= F16_REL_TOL
+    B, T, N, K, H = 2, 64, 8, 2, 64
+    q = f16_round(rng.standard_normal((B, T, N, H)))
+    k, v = (f16_round(rng.standard_normal((B, T, K, H))) for _ in range(2))
+    bias = rng.standard_normal((B, 1, 1, T)) * 0.5  # the module's [B,1,1,S] f32 bias
+    bias[1, ..., 40:] = -np.inf
+    (o,) = run(client, M.dot_product_attention_module(B=B, T=T, N=N, K=K, H=H, dt="f16", is_causal=False,
+                                                      bias=True), [q, k, v, bias], ["f16"] * 3 + ["f32"])
+    tr = lambda a: a.transpose(0, 2, 1, 3)  # noqa: E731
+    ref = tr(oracle.sdpa(tr(q), tr(k), tr(v), 1 / math.sqrt(H), mask=bias))
+    assert rel_inf(o, ref) <= F16_REL_TOL
+    S = 1024
+    q = f16_round(rng.standard_normal((2, 32, 1, 128)))
+    k, v = (f16_round(rng.standard_normal((2, 8, S, 128))) for _ in range(2))
+    lens = np.array([1024, 300])
+    mask = np.where(np.arange(S)[None] < lens[:, None], 0.0, -np.inf).reshape(2, 1, 1, S)
+    (o,) = run(client, M.gqa_decode_module(B=2, S=S, dt="f16"), [q, k, v, mask], ["f16", "f16", "f16", "f32"])
+    qn = f16_round(oracle.rms_norm(q, None, 1e-6))
+    assert rel_inf(o, oracle.sdpa(qn, k, v, 1 / math.sqrt(128), mask=mask)) <= F16_REL_TOL
+
+
+def test_f16_backward_custom_calls_through_pjrt(client, oracle):
+    rng = np.random.default_rng(93)
+    B, T, N, K, H = 1, 128, 8, 2, 128
+    q, g = (f16_round(rng.standard_normal((B, T, N, H))) for _ in range(2))
+    k, v = (f16_round(rng.standard_normal((B, T, K, H))) for _ in range(2))
+    outs = run(client, M.custom_call_sdpa_bwd_module(B=B, T=T, N=N, K=K, H=H, dt="f16", scale=0.1),
+               [q, k, v, g], ["f16"] * 4)
+    tr = lambda a: a.transpose(0, 2, 1, 3)  # noqa: E731
+    refs = oracle.sdpa_bwd(tr(q), tr(k), tr(v), tr(g), 0.1)
+    for o, r in zip(outs, refs):
+        assert rel_inf(o, tr(r)) <= F16_REL_TOL
+    x, dy = (f16_round(rng.standard_normal((16, 64, 768))) for _ in range(2))
+    w = f16_round(1 + 0.1 * rng.standard_normal(768))
+    b = f16_round(0.1 * rng.standard_normal(768))
+    outs = run(client, M.custom_call_layer_norm_bwd_module(shape=(16, 64, 768), eps=1e-5, dt="f16"),
+               [x, w, b, dy], ["f16"] * 4)
+    refs = oracle.layer_norm_bwd(x.reshape(-1, 768), w, dy.reshape(-1, 768), 1e-5)
+    for o, r in zip(outs, refs):
+        assert rel_inf(o.reshape(r.shape), r) <= F16_REL_TOL
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 def test_sdpa_vjp_module_linked(client, dt):
     """jax.vjp of mlx_dot_product_attention as one module: the plan hands the
     forward's output and lse to the backward (no recompute).  Every result
@@ -564,8 +642,8 @@ def test_sdpa_vjp_module_linked(client, dt):
     rng = np.random.default_rng(41)
     B, T, N, H = 2, 128, 4, 64
     q, k, v, g = (rng.standard_normal((B, T, N, H)).astype(np.float32) for _ in range(4))
-    if dt == "bf16":
-        q, k, v, g = (bf16_round(a) for a in (q, k, v, g))
+    if dt != "f32":
+        q, k, v, g = (bf16_round(a) if dt == "bf16" else f16_round(a) for a in (q, k, v, g))
     linked = run(client, M.sdpa_vjp_module(B=B, T=T, N=N, H=H, dt=dt), [q, k, v, g], [dt] * 4)
     plain = run(client, M.sdpa_vjp_module(B=B, T=T, N=N, H=H, dt=dt, same_inputs=False), [q, k, v, g, q],
                 [dt] * 5)
