@@ -119,9 +119,13 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
 
 const char* kind_name(const Plan& pl) {
   switch (pl.kind) {
-    case Kind::kFlashBf16:
-      if (pl.p.dtype == MFX_F16) return pl.p.D == 128 ? "flash_f16_d128" : "flash_f16_d64";
-      return pl.p.D == 128 ? "flash_bf16_d128" : "flash_bf16_d64";
+    case Kind::kFlashBf16: {
+      static const char* const names[2][4] = {
+          {"flash_bf16_d32", "flash_bf16_d64", "flash_bf16_d96", "flash_bf16_d128"},
+          {"flash_f16_d32", "flash_f16_d64", "flash_f16_d96", "flash_f16_d128"}};
+      const int d = pl.p.D;
+      return names[pl.p.dtype == MFX_F16][d == 32 ? 0 : d == 64 ? 1 : d == 96 ? 2 : 3];
+    }
     case Kind::kFlashF32:
       if (flash_f32_use_split(pl.p)) return pl.p.D == 128 ? "flash_f32_split_d128" : "flash_f32_split_d64";
       return pl.p.D == 128 ? "flash_f32_d128" : "flash_f32_d64";

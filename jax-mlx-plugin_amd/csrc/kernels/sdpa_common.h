@@ -70,6 +70,7 @@ int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s);
 // Kernel families; each returns MFX_OK or an error code after launching.
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s);
 int launch_flash_bf16_pipe(const SdpaParams& p, hipStream_t s);  // no mask
+int launch_flash_bf16_pipe_wide(const SdpaParams& p, hipStream_t s);  // head sizes 32, 96
 int launch_flash_f32(const SdpaParams& p, hipStream_t s);
 int launch_decode(const SdpaParams& p, hipStream_t s);
 int launch_decode_mfma(const SdpaParams& p, hipStream_t s);

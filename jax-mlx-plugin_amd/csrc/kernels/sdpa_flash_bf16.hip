@@ -322,7 +322,10 @@ bool flash_bf16_supports(const SdpaParams& p) {
   // inside it and the last row's tail outside).
   if (p.ks[2] < p.D || p.vs[2] < p.Dv) return false;
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
-  if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
+  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128)) return false;
+  // Masks that vary along query rows run on this file's kernel: head sizes
+  // 64 and 128 only.
+  if (p.mask && p.ms[2] != 0 && p.Tq > 1 && p.D != 64 && p.D != 128) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.os[i] % 4) return false;
@@ -333,8 +336,9 @@ bool flash_bf16_supports(const SdpaParams& p) {
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s) {
   // Without an additive mask, or with one that does not vary along query
   // rows, the software-pipelined kernel runs (sdpa_flash_bf16_pipe.hip);
-  // this file's kernel serves masks with a query-row stride.
-  if (!p.mask || p.ms[2] == 0) return launch_flash_bf16_pipe(p, s);
+  // this file's kernel serves masks with a query-row stride.  (With one
+  // query row the pipelined kernel's mask row is that row.)
+  if (!p.mask || p.ms[2] == 0 || p.Tq == 1) return launch_flash_bf16_pipe(p, s);
   if (p.dtype == MFX_F16) return p.D == 128 ? launch_d<128, 1>(p, s) : launch_d<64, 1>(p, s);
   return p.D == 128 ? launch_d<128, 0>(p, s) : launch_d<64, 0>(p, s);
 }

@@ -193,18 +193,29 @@ struct Loader {
 constexpr int wait_k(int j, int MS, int pf) { return pf < MS - 1 - j ? pf : MS - 1 - j; }
 constexpr int wait_v(int j, int MP, int pf) { return 2 * (pf < MP - 1 - j ? pf : MP - 1 - j); }
 
-template <int D, bool CAUSAL, int MT, int E>
+// D: features per row of the LDS tiles (64 or 128); DV <= D: the head size,
+// a multiple of 32.  Rows are loaded D wide, and only features below DV
+// reach an MFMA: S contracts over DV features (DV/16 k-steps) and O has DV/32
+// feature blocks, so the features DV .. D-1 of a tile (the next row's first
+// elements, or zeros past the tensor) are never read from LDS.  (256-wide
+// rows do not fit: the loop's state passes 512 registers.)
+template <int D, int DV, bool CAUSAL, int MT, int E>
 __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
+  static_assert(DV % 32 == 0 && DV <= D && D - DV < 64, "head size");
   constexpr int TILE = kBN * D;     // elements of one K or V tile
   constexpr int TB = TILE * 2;      // its bytes
-  constexpr int MS = 2 * (D / 16);  // S MFMAs per tile
-  constexpr int MP = 4 * (D / 32);  // PV MFMAs per tile
+  constexpr int MS = 2 * (DV / 16);  // S MFMAs per tile
+  constexpr int MP = 4 * (DV / 32);  // PV MFMAs per tile
+  // LDS read offsets are 16-bit immediates: tiles wider than 128 features
+  // would put the V stages past 64 KB, addressed from a per-lane base that
+  // includes their start.
+  constexpr int VA0 = D > 128 ? 2 * TB : 0;
   constexpr bool MASK = MT != 0;
   // Operand reads ahead of their MFMA: 2, 4 and 6 measured alike on config
   // 3; a masked kernel keeps 2 for the registers its mask rows take.
   constexpr int PFK = MASK ? 2 : kPfK, PFV = MASK ? 2 : kPfV;
   constexpr float kSumCap = kMaxP<E>;
-  static_assert(MS % 8 == 0 || 8 % MS == 0, "interleave");
+  static_assert(MS >= 4 && MP >= 4, "the 8 exp2 pairs of a phase spread over its MFMAs");
   __shared__ __attribute__((aligned(16))) bf16 smem[4 * TILE];  // K0 K1 V0 V1
   // Mask rows (raw score units) of the tiles in K stages 0 / 1 (MASK only):
   // an array of its own, so the compiler's reads of it need no wait for the
@@ -321,11 +332,11 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   }
 
   // Q rows as the B operand (rows past Tq read a valid row and are zeroed).
-  bf16x8 qf[D / 16];
+  bf16x8 qf[DV / 16];
   {
     const bf16* qrow = qp + (int64_t)min(qi, Tq - 1) * qs2 + half * 8;
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
+    for (int kk = 0; kk < DV / 16; ++kk) {
       u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + kk * 16);
       if (qi >= Tq) raw = u32x4{0u, 0u, 0u, 0u};
       qf[kk] = __builtin_bit_cast(bf16x8, raw);
@@ -335,13 +346,13 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   // LDS byte addresses of the operand reads; the stage, the 32-key block of
   // the K tile and the 16-key step of the V tile are immediate offsets.
   const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem;
-  uint32_t ka[D / 16];
+  uint32_t ka[DV / 16];
   {
     const int k_sw = tile_swz<D>(l32);
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) ka[kk] = base + (uint32_t)((l32 * D + ((kk * 2 + half) ^ k_sw) * 8) * 2);
+    for (int kk = 0; kk < DV / 16; ++kk) ka[kk] = base + (uint32_t)((l32 * D + ((kk * 2 + half) ^ k_sw) * 8) * 2);
   }
-  uint32_t va[D / 32][2];
+  uint32_t va[DV / 32][2];
   {
     // Transposing reads: 16 lanes x 4 keys per read; k-slots 0-3 are keys
     // 4*half + e of the 16-key step, slots 4-7 the same + 8.
@@ -351,15 +362,15 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     const int v_chunk = tg * 2 + ((tj & 3) >> 1);
     const int v_sub = (tj & 1) * 4;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-      va[dt][0] = base + (uint32_t)((v_row * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw) * 8) * 2);
-      va[dt][1] = base + (uint32_t)(((v_row + 8) * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw8) * 8) * 2);
+    for (int dt = 0; dt < DV / 32; ++dt) {
+      va[dt][0] = base + VA0 + (uint32_t)((v_row * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw) * 8) * 2);
+      va[dt][1] = base + VA0 + (uint32_t)(((v_row + 8) * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw8) * 8) * 2);
     }
   }
 
-  f32x16 o[D / 32];
+  f32x16 o[DV / 32];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
   // Running exp2 base of the row (log2 units, shared by lanes l and l^32),
@@ -429,7 +440,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     nbase = -b_run;
     l_run *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
     float a0 = 0.f, a1 = 0.f;
@@ -464,7 +475,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   auto tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pc)[2], u32x4 (&pn)[2], int t, auto ks_tag,
                   auto vs_tag) {
     constexpr int KS = decltype(ks_tag)::value;
-    constexpr int VB = (2 + decltype(vs_tag)::value) * TB;
+    constexpr int VB = (2 + decltype(vs_tag)::value) * TB - VA0;
     bf16x8 kr[MS];
     s16x4 vr[MP][2];
     auto rdk = [&](auto j_tag) {  // S MFMA j: 32-key block j & 1, d-slice j >> 1
@@ -472,9 +483,9 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
       if constexpr ((j & 1) == 0) ds_b128<KS * TB>(kr[j], ka[j >> 1]);
       else ds_b128<KS * TB + 32 * D * 2>(kr[j], ka[j >> 1]);
     };
-    auto rdv = [&](auto j_tag) {  // PV MFMA j: d-block j % (D/32), 16-key step j / (D/32)
+    auto rdv = [&](auto j_tag) {  // PV MFMA j: d-block j % (DV/32), 16-key step j / (DV/32)
       constexpr int j = decltype(j_tag)::value;
-      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      constexpr int dt = j % (DV / 32), ks = j / (DV / 32);
       ds_tr<VB + ks * 16 * D * 2>(vr[j][0], va[dt][0]);
       ds_tr<VB + ks * 16 * D * 2>(vr[j][1], va[dt][1]);
     };
@@ -514,7 +525,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     fence();
     static_for<0, MP>([&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
-      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      constexpr int dt = j % (DV / 32), ks = j / (DV / 32);
       if constexpr (j + PFV < MP) rdv(std::integral_constant<int, j + PFV>{});
       lgkm_tie<wait_v(j, MP, PFV)>(vr[j][0], vr[j][1]);
       const bf16x8 a =
@@ -534,9 +545,9 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     s16x4 vr[MP][2];
     auto rdv = [&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
-      constexpr int dt = j % (D / 32), ks = j / (D / 32);
-      ds_tr<2 * TB + ks * 16 * D * 2>(vr[j][0], va[dt][0] + vs_bytes);
-      ds_tr<2 * TB + ks * 16 * D * 2>(vr[j][1], va[dt][1] + vs_bytes);
+      constexpr int dt = j % (DV / 32), ks = j / (DV / 32);
+      ds_tr<2 * TB - VA0 + ks * 16 * D * 2>(vr[j][0], va[dt][0] + vs_bytes);
+      ds_tr<2 * TB - VA0 + ks * 16 * D * 2>(vr[j][1], va[dt][1] + vs_bytes);
     };
     static_for<0, PFV>(rdv);
     fence();
@@ -549,7 +560,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     lf = 0.f;
     static_for<0, MP>([&](auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
-      constexpr int dt = j % (D / 32), ks = j / (D / 32);
+      constexpr int dt = j % (DV / 32), ks = j / (DV / 32);
       if constexpr (j + PFV < MP) rdv(std::integral_constant<int, j + PFV>{});
       lgkm_tie<wait_v(j, MP, PFV)>(vr[j][0], vr[j][1]);
       const bf16x8 a =
@@ -635,7 +646,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   if (qi < Tq) {
     bf16* orow = op + qi * os2;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u16x4 w;
@@ -647,46 +658,66 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   PHASE(fence(); ph.write(lane, id * kNW + wave, bh, mblk, N, nw, c_epi);)
 }
 
-template <int D, bool CAUSAL, int MT, int E>
+template <int D, int DV, bool CAUSAL, int MT, int E>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   const int nmb = (p.Tq + kBM - 1) / kBM;
   const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
-  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, CAUSAL, MT, E>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
+  hipLaunchKernelGGL((flash_bf16_pipe_kernel<D, DV, CAUSAL, MT, E>), dim3((unsigned)blocks), dim3(kNT), 0, s, p);
   return launch_status("flash_bf16_pipe_kernel");
 }
 
-template <int D, int MT, int E>
+template <int D, int DV, int MT, int E>
 int launch_c(const SdpaParams& p, hipStream_t s) {
-  return p.causal ? launch_t<D, true, MT, E>(p, s) : launch_t<D, false, MT, E>(p, s);
+  return p.causal ? launch_t<D, DV, true, MT, E>(p, s) : launch_t<D, DV, false, MT, E>(p, s);
 }
 
-template <int D, int E>
+template <int D, int DV, int E>
 int launch_m(const SdpaParams& p, hipStream_t s) {
-  if (!p.mask) return launch_c<D, 0, E>(p, s);
+  if (!p.mask) return launch_c<D, DV, 0, E>(p, s);
 #if defined(MFX_PHASE_TIMERS)
   // The diagnostic build instruments the mask-free kernels only.
   return fail(MFX_E_UNSUPPORTED, "phase-timer build: masked attention is not instrumented");
 #else
-  if (p.mask_dtype == MFX_F32) return launch_c<D, 1, E>(p, s);
-  if (p.mask_dtype == MFX_BF16) return launch_c<D, 2, E>(p, s);
-  return launch_c<D, 3, E>(p, s);
+  if (p.mask_dtype == MFX_F32) return launch_c<D, DV, 1, E>(p, s);
+  if (p.mask_dtype == MFX_BF16) return launch_c<D, DV, 2, E>(p, s);
+  return launch_c<D, DV, 3, E>(p, s);
 #endif
 }
 
+#if defined(MFX_PIPE_WIDE)
+// Head sizes 32 (64-wide tiles) and 96 (128-wide tiles).
 template <int E>
 int launch_d(const SdpaParams& p, hipStream_t s) {
-  if (p.D == 128) return launch_m<128, E>(p, s);
-  return launch_m<64, E>(p, s);
+  if (p.D == 32) return launch_m<64, 32, E>(p, s);
+  return launch_m<128, 96, E>(p, s);
 }
+#else
+template <int E>
+int launch_d(const SdpaParams& p, hipStream_t s) {
+  if (p.D == 128) return launch_m<128, 128, E>(p, s);
+  if (p.D == 64) return launch_m<64, 64, E>(p, s);
+  return launch_flash_bf16_pipe_wide(p, s);
+}
+#endif
 
 }  // namespace
 
+#if defined(MFX_PIPE_WIDE)
+// Head sizes 32 and 96 of launch_flash_bf16_pipe (their kernels are
+// instantiated in a translation unit of their own, so the two compile in
+// parallel).
+int launch_flash_bf16_pipe_wide(const SdpaParams& p, hipStream_t s) {
+  return p.dtype == MFX_F16 ? launch_d<1>(p, s) : launch_d<0>(p, s);
+}
+#else
 // Flash attention without an additive mask or with one that does not vary
 // along query rows, p.ms[2] == 0 (the caller checked flash_bf16_supports);
-// q, k, v and out all bf16 or all f16 (p.dtype).
+// q, k, v and out all bf16 or all f16 (p.dtype); head size 32, 64, 96 or
+// 128.
 int launch_flash_bf16_pipe(const SdpaParams& p, hipStream_t s) {
   return p.dtype == MFX_F16 ? launch_d<1>(p, s) : launch_d<0>(p, s);
 }
+#endif
 
 }  // namespace mfx
 

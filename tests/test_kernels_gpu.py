@@ -909,3 +909,44 @@ def test_sdpa_bwd_from_forward_residuals(cuda, dt, shape, causal, layout, group)
     want = (m[..., 0] + np.log(np.exp(s - m).sum(-1))) / np.log(2.0)
     err = np.abs(lse.cpu().numpy().reshape(B, H, T) - want).max()
     assert err <= (2.0 ** -9 / np.log(2.0) if dt == "bf16" else 1e-4), err
+
+
+# ------------------------------------------------------ head sizes 32, 96
+# The pipelined flash kernel at head sizes 32 (64-wide LDS tiles) and 96
+# (128-wide): rows load tile-wide, and only the head's features reach an
+# MFMA (DV/16 S k-steps, DV/32 output blocks).  Ragged, causal and GQA
+# shapes, plus a row-shared padding mask, against the fp64 oracle; f16 at
+# its 5e-3 bar.
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [32, 96])
+@pytest.mark.parametrize("tq,tk,hq,hkv,causal", [(100, 77, 3, 3, False), (100, 77, 4, 2, True),
+                                                 (77, 200, 2, 1, True), (129, 129, 3, 3, True),
+                                                 (1000, 1000, 2, 2, False), (7, 300, 4, 4, False)])
+def test_sdpa_flash_head_sizes_32_96(cuda, nat, oracle, dtype, D, tq, tk, hq, hkv, causal):
+    td = cuda.bfloat16 if dtype == "bf16" else cuda.float16
+    q, k, v = make_qkv(cuda, 71, (2, hq, tq, D), (2, hkv, tk, D), td)
+    assert nat.sdpa_kernel_name(q, k, v, causal=causal) == f"flash_{dtype}_d{D}"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, causal=causal)
+    ref = oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=causal)
+    r = rel_inf(host(out), ref)
+    assert r <= (BF16_REL_TOL if dtype == "bf16" else 5e-3), r
+
+
+@pytest.mark.parametrize("D", [32, 96])
+def test_sdpa_flash_head_sizes_32_96_mask_and_layout(cuda, nat, oracle, D):
+    """BTNH views of packed rows (row stride above D: the tile-wide loads
+    read the next head's features, which no MFMA uses) with a padding mask."""
+    rng = np.random.default_rng(72)
+    B, T, Hq, Hkv = 2, 150, 8, 2
+    q = dev(cuda, rng.standard_normal((B, T, Hq, D)), cuda.bfloat16)
+    kv = dev(cuda, rng.standard_normal((B, T, 2 * Hkv, D)), cuda.bfloat16)
+    k, v = kv[:, :, :Hkv], kv[:, :, Hkv:]
+    lens = np.array([150, 61])
+    mask = np.where(np.arange(T)[None] < lens[:, None], 0.0, -np.inf).reshape(B, 1, 1, T)
+    maskd = dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd, layout="bthd") == f"flash_bf16_d{D}"
+    out = nat.sdpa(q, k, v, scale=0.2, mask=maskd, layout="bthd")
+    qh, kh, vh = (host(t).transpose(0, 2, 1, 3) for t in (q, k, v))
+    ref = oracle.sdpa(qh, kh, vh, 0.2, mask=mask).transpose(0, 2, 1, 3)
+    check_sdpa(out, ref, "bf16")
