@@ -74,6 +74,7 @@ int launch_flash_bf16_pipe_wide(const SdpaParams& p, hipStream_t s);  // head si
 int launch_flash_f32(const SdpaParams& p, hipStream_t s);
 int launch_decode(const SdpaParams& p, hipStream_t s);
 int launch_decode_mfma(const SdpaParams& p, hipStream_t s);
+int launch_decode_mfma_wide(const SdpaParams& p, hipStream_t s);  // head sizes 32, 96
 int launch_decode_combine(const SdpaParams& p, hipStream_t s);  // merges split partials
 int launch_generic(const SdpaParams& p, hipStream_t s);
 

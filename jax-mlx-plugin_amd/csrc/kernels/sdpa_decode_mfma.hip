@@ -98,6 +98,33 @@ __device__ __forceinline__ void lgkm_wait_tied(s16x4 (&v)[2][2][2]) {
                : "memory");
 }
 
+// The same for other fragment counts (head sizes 32 and 96): the wait, then
+// one tie per register, all volatile and so kept in this order.
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied_n(bf16x8 (&a)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(a[i]));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied_n(s16x4 (&v)[N][2][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(v[i][j >> 1][j & 1]));
+}
+template <int N>
+__device__ __forceinline__ void wait_frags(bf16x8 (&a)[N]) {
+  if constexpr (N == 8 || N == 4) lgkm_wait_tied(a);
+  else lgkm_wait_tied_n(a);
+}
+template <int N>
+__device__ __forceinline__ void wait_frags(s16x4 (&v)[N][2][2]) {
+  if constexpr (N == 4 || N == 2) lgkm_wait_tied(v);
+  else lgkm_wait_tied_n(v);
+}
+
 // s_waitcnt vmcnt(N) with the other counters left alone (N < 64).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -186,8 +213,12 @@ __global__ __launch_bounds__(256) void decode_tiles_kernel(SdpaParams p) {
 // First element of wavefront w's range of the concatenated tile lists.
 __device__ __forceinline__ int64_t range_start(int w, int64_t T, int W) { return (int64_t)w * T / W; }
 
-template <int D, int MT, bool MB, bool CAUSAL, int E>
+// D: features per row of the LDS tiles (64 or 128); DV <= D: the head size
+// (a multiple of 32).  Rows load D wide and only features below DV reach an
+// MFMA, as in the pipelined prefill kernel.
+template <int D, int DV, int MT, bool MB, bool CAUSAL, int E>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
+  static_assert(DV % 32 == 0 && DV <= D && D - DV < 64, "head size");
   constexpr bool MASK = MT != 0;
   using Loader = tiles::TileLoader<D, kDN, 1>;
   constexpr int kMS = mask_slots<MT, MB>();
@@ -268,19 +299,19 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 
   // Per-lane byte offsets of the operand reads within a tile (the same
   // patterns as the prefill kernel).
-  uint32_t k_addr[D / 16];
-  uint32_t v_addr[D / 32][2];
+  uint32_t k_addr[DV / 16];
+  uint32_t v_addr[DV / 32][2];
   {
     const int k_sw = tile_swz<D>(col);
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) k_addr[kk] = (uint32_t)((col * D + ((kk * 2 + half) ^ k_sw) * 8) * 2);
+    for (int kk = 0; kk < DV / 16; ++kk) k_addr[kk] = (uint32_t)((col * D + ((kk * 2 + half) ^ k_sw) * 8) * 2);
     const int tj = lane & 15, tg = (lane >> 4) & 1;
     const int v_row = 4 * half + (tj >> 2);
     const int v_sw = tile_swz<D>(v_row), v_sw8 = tile_swz<D>(v_row + 8);
     const int v_chunk = tg * 2 + ((tj & 3) >> 1);
     const int v_sub = (tj & 1) * 4;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
+    for (int dt = 0; dt < DV / 32; ++dt) {
       v_addr[dt][0] = (uint32_t)((v_row * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw) * 8) * 2);
       v_addr[dt][1] = (uint32_t)(((v_row + 8) * D + v_sub + ((dt * 4 + v_chunk) ^ v_sw8) * 8) * 2);
     }
@@ -318,14 +349,14 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     // host.)
     const bool qnorm = p.q_rms_eps >= 0.f;
     const bf16* wq = static_cast<const bf16*>(p.q_rms_weight);
-    bf16x8 qf[D / 16], wf[D / 16];
+    bf16x8 qf[DV / 16], wf[DV / 16];
     {
       const bf16* qrow = static_cast<const bf16*>(p.q) + b * p.qs[0] + hq * p.qs[1] + tq * p.qs[2] + half * 8;
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + kk * 16);
+      for (int kk = 0; kk < DV / 16; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + kk * 16);
       if (qnorm && wq) {
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) wf[kk] = *reinterpret_cast<const bf16x8*>(wq + kk * 16 + half * 8);
+        for (int kk = 0; kk < DV / 16; ++kk) wf[kk] = *reinterpret_cast<const bf16x8*>(wq + kk * 16 + half * 8);
       }
     }
     // Mask element offset of the row each lane gathers in each mask
@@ -344,9 +375,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
     const Loader kload(kp, p.ks[2], Tk, 0, lane), vload(vp, p.vs[2], Tk, 0, lane);
 
-    f32x16 o[D / 32];
+    f32x16 o[DV / 32];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
     float b_run = -INFINITY, l_run = 0.f;
@@ -433,26 +464,26 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       f32x16 sc[kMT];
 #pragma unroll
       for (int mt = 0; mt < kMT; ++mt) {
-        bf16x8 ka[D / 16];
+        bf16x8 ka[DV / 16];
         const uint32_t kbase = lds_addr(kc) + mt * 32 * D * 2;
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk)
+        for (int kk = 0; kk < DV / 16; ++kk)
           asm volatile("ds_read_b128 %0, %1" : "=v"(ka[kk]) : "v"(kbase + k_addr[kk]));
-        lgkm_wait_tied(ka);
+        wait_frags(ka);
 #pragma unroll
         for (int i = 0; i < 16; ++i) sc[mt][i] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk)
+        for (int kk = 0; kk < DV / 16; ++kk)
           sc[mt] = mfma16<E>(ka[kk], qf[kk], sc[mt]);
       }
       // V^T operand reads (transposing), issued now so that their latency
       // overlaps the softmax; inline asm for the same reason as the K reads.
       static_assert(kKS == 2, "two 16-key halves per tile");
-      s16x4 vr[D / 32][kKS][2];
+      s16x4 vr[DV / 32][kKS][2];
       {
         const uint32_t vbase = lds_addr(vc);
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vr[dt][0][h]) : "v"(vbase + v_addr[dt][h]));
@@ -484,7 +515,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         b_run = nb;
         l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
       }
@@ -525,9 +556,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         for (int j = 0; j < kKS; ++j) pb[j] = __builtin_bit_cast(bf16x8, pw[j]);
         l_run += l0 + l1;
       }
-      lgkm_wait_tied(vr);
+      wait_frags(vr);
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
         for (int ks = 0; ks < kKS; ++ks) {
           const bf16x8 a =
@@ -545,12 +576,12 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     // Rows past R are zero (never stored); optional RMSNorm in fp32, rounded
     // to bf16 as the unfused graph rounds its output.
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
+    for (int kk = 0; kk < DV / 16; ++kk)
       if (!qvalid) qf[kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
     if (qnorm && E == 0) {
       float ss = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)
+      for (int kk = 0; kk < DV / 16; ++kk)
 #pragma unroll
         for (int e2 = 0; e2 < 8; ++e2) {
           const float x = static_cast<float>(qf[kk][e2]);
@@ -558,9 +589,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         }
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
       ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
+      const float inv = rsqrtf(ss / (float)DV + p.q_rms_eps);
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)
+      for (int kk = 0; kk < DV / 16; ++kk)
 #pragma unroll
         for (int e2 = 0; e2 < 8; ++e2) {
           const float wv = wq ? static_cast<float>(wf[kk][e2]) : 1.f;
@@ -570,7 +601,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       // f16: whole fragments converted (see frag_f32_f16).
       float ss = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
+      for (int kk = 0; kk < DV / 16; ++kk) {
         float x[8];
         frag_f32_f16(qf[kk], x);
 #pragma unroll
@@ -578,9 +609,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       }
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
       ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      const float inv = rsqrtf(ss / (float)D + p.q_rms_eps);
+      const float inv = rsqrtf(ss / (float)DV + p.q_rms_eps);
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
+      for (int kk = 0; kk < DV / 16; ++kk) {
         float x[8], w[8];
         frag_f32_f16(qf[kk], x);
         if (wq) frag_f32_f16(wf[kk], w);
@@ -604,13 +635,13 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
     if (qvalid) {
-      float* part = p.partial + ((int64_t)(w + bhk) * R + rr) * (D + 2);
+      float* part = p.partial + ((int64_t)(w + bhk) * R + rr) * (DV + 2);
       if (half == 0) {
         part[0] = b_run;
         part[1] = lt;
       }
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
@@ -632,7 +663,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 // unfused softmax.
 template <typename OT, int D>
 __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
-  constexpr int NQ = D / 64;  // features per lane
+  constexpr int NQ = (D + 63) / 64;  // features per lane (lane + 64 q < D)
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*Hq + h)*Tq + t
   const int64_t rows_total = (int64_t)p.B * p.Hq * p.Tq;
@@ -674,7 +705,8 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   OT* orow = static_cast<OT*>(p.out) + b * p.os[0] + h * p.os[1] + tq * p.os[2];
   if (cnt == 0) {
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) orow[lane + 64 * q] = from_f32<OT>(__builtin_nanf(""));
+    for (int q = 0; q < NQ; ++q)
+      if ((D % 64 == 0 || lane + 64 * q < D)) orow[lane + 64 * q] = from_f32<OT>(__builtin_nanf(""));
     return;
   }
   // Wavefronts whose range [start(w), start(w+1)) meets [P, P + cnt).
@@ -693,7 +725,7 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
   for (int u = 0; u < 16; ++u) {
     const float* pk = slot_ptr(min(u, nslot - 1));
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) vf[u][q] = pk[2 + lane + 64 * q];
+    for (int q = 0; q < NQ; ++q) vf[u][q] = (D % 64 == 0 || lane + 64 * q < D) ? pk[2 + lane + 64 * q] : 0.f;
   }
   // Lane k of a 64-slot chunk holds slot k0 + k: whether its wavefront's
   // range is non-empty (the next lane's start differs) and its (m, l).
@@ -752,14 +784,15 @@ __global__ __launch_bounds__(256) void decode_bal_combine_kernel(SdpaParams p) {
       for (int u = 0; u < 16; ++u) {
         const float* pk = slot_ptr(k0 + min(j0 + u, n - 1));
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) v[u][q] = pk[2 + lane + 64 * q];
+        for (int q = 0; q < NQ; ++q) v[u][q] = (D % 64 == 0 || lane + 64 * q < D) ? pk[2 + lane + 64 * q] : 0.f;
       }
       accumulate(v, sc, j0, n);
     }
   }
   const float inv = 1.0f / l;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) orow[lane + 64 * q] = from_f32<OT>(acc[q] * inv);
+  for (int q = 0; q < NQ; ++q)
+    if ((D % 64 == 0 || lane + 64 * q < D)) orow[lane + 64 * q] = from_f32<OT>(acc[q] * inv);
 }
 
 // Whether every query row of a kv head sees the same mask row (the mask is
@@ -769,44 +802,46 @@ bool mask_rows_shared(const SdpaParams& p) {
   return (p.ms[1] == 0 || p.group == 1) && (p.ms[2] == 0 || p.Tq == 1);
 }
 
-template <int D, int MT, bool MB, bool CAUSAL, int E>
+template <int D, int DV, int MT, bool MB, bool CAUSAL, int E>
 int launch_t(const SdpaParams& p, hipStream_t s) {
   hipLaunchKernelGGL((decode_tiles_kernel<MT, CAUSAL>), dim3((unsigned)(p.B * p.Hkv)), dim3(256), 0, s, p);
   int rc = launch_status("decode_tiles_kernel");
   if (rc != MFX_OK) return rc;
-  hipLaunchKernelGGL((decode_mfma_kernel<D, MT, MB, CAUSAL, E>), dim3((unsigned)p.num_splits), dim3(64), 0, s, p);
+  hipLaunchKernelGGL((decode_mfma_kernel<D, DV, MT, MB, CAUSAL, E>), dim3((unsigned)p.num_splits), dim3(64), 0, s,
+                     p);
   if ((rc = launch_status("decode_mfma_kernel")) != MFX_OK) return rc;
   const unsigned blocks = (unsigned)(((int64_t)p.B * p.Hq * p.Tq + 3) / 4);
   using OT = std::conditional_t<E == 0, bf16, _Float16>;
-  hipLaunchKernelGGL((decode_bal_combine_kernel<OT, D>), dim3(blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((decode_bal_combine_kernel<OT, DV>), dim3(blocks), dim3(256), 0, s, p);
   return launch_status("decode_bal_combine_kernel");
 }
 
-template <int D, int MT, bool CAUSAL, int E>
+template <int D, int DV, int MT, bool CAUSAL, int E>
 int launch_m(const SdpaParams& p, hipStream_t s) {
-  if constexpr (MT == 0) return launch_t<D, 0, true, CAUSAL, E>(p, s);
+  if constexpr (MT == 0) return launch_t<D, DV, 0, true, CAUSAL, E>(p, s);
   else
-    return mask_rows_shared(p) ? launch_t<D, MT, true, CAUSAL, E>(p, s) : launch_t<D, MT, false, CAUSAL, E>(p, s);
+    return mask_rows_shared(p) ? launch_t<D, DV, MT, true, CAUSAL, E>(p, s)
+                               : launch_t<D, DV, MT, false, CAUSAL, E>(p, s);
 }
 
-template <int D, bool CAUSAL, int E>
+template <int D, int DV, bool CAUSAL, int E>
 int launch_c(const SdpaParams& p, hipStream_t s) {
   switch (p.mask ? mask_code(p.mask_dtype) : 0) {
-    case 1: return launch_m<D, 1, CAUSAL, E>(p, s);
-    case 2: return launch_m<D, 2, CAUSAL, E>(p, s);
-    case 3: return launch_m<D, 3, CAUSAL, E>(p, s);
-    default: return launch_m<D, 0, CAUSAL, E>(p, s);
+    case 1: return launch_m<D, DV, 1, CAUSAL, E>(p, s);
+    case 2: return launch_m<D, DV, 2, CAUSAL, E>(p, s);
+    case 3: return launch_m<D, DV, 3, CAUSAL, E>(p, s);
+    default: return launch_m<D, DV, 0, CAUSAL, E>(p, s);
   }
 }
 
-template <int D, int E>
+template <int D, int DV, int E>
 int launch_e(const SdpaParams& p, hipStream_t s) {
-  return p.causal ? launch_c<D, true, E>(p, s) : launch_c<D, false, E>(p, s);
+  return p.causal ? launch_c<D, DV, true, E>(p, s) : launch_c<D, DV, false, E>(p, s);
 }
 
-template <int D>
+template <int D, int DV>
 int launch_d(const SdpaParams& p, hipStream_t s) {
-  return p.dtype == MFX_F16 ? launch_e<D, 1>(p, s) : launch_e<D, 0>(p, s);
+  return p.dtype == MFX_F16 ? launch_e<D, DV, 1>(p, s) : launch_e<D, DV, 0>(p, s);
 }
 
 template <int D>
@@ -819,10 +854,17 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
 
+#if defined(MFX_DECODE_WIDE)
+// Head sizes 32 (64-wide tiles) and 96 (128-wide tiles) of
+// launch_decode_mfma, instantiated in a translation unit of their own.
+int launch_decode_mfma_wide(const SdpaParams& p, hipStream_t s) {
+  return p.D == 32 ? launch_d<64, 32>(p, s) : launch_d<128, 96>(p, s);
+}
+#else
 bool decode_mfma_supports(const SdpaParams& p) {
   if (p.dtype != MFX_BF16 && p.dtype != MFX_F16) return false;
   if (!(p.scale_log2 > 0.f)) return false;
-  if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
+  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128)) return false;
   if (p.group * p.Tq > 32) return false;
   if ((int64_t)p.B * p.Hkv * ((p.Tk + kDN - 1) / kDN) >= (1LL << 31)) return false;  // tile lists
   // Buffer-resource extents span Tk forward rows of at least D elements each.
@@ -850,7 +892,7 @@ int decode_mfma_tile() { return kDN; }
 int decode_mfma_resident(const SdpaParams& p) {
   // Workgroups (one wavefront each) that fit the 160 KB of LDS of a CU, on
   // 256 CUs.
-  const int lds = p.D == 128 ? lds_bytes_d<128>(p) : lds_bytes_d<64>(p);
+  const int lds = p.D > 64 ? lds_bytes_d<128>(p) : lds_bytes_d<64>(p);
   return 256 * (160 * 1024 / lds);
 }
 
@@ -875,7 +917,10 @@ void decode_mfma_bind(SdpaParams& p, int W, void* ws) {
 }
 
 int launch_decode_mfma(const SdpaParams& p, hipStream_t s) {
-  return p.D == 128 ? launch_d<128>(p, s) : launch_d<64>(p, s);
+  if (p.D == 128) return launch_d<128, 128>(p, s);
+  if (p.D == 64) return launch_d<64, 64>(p, s);
+  return launch_decode_mfma_wide(p, s);
 }
+#endif
 
 }  // namespace mfx

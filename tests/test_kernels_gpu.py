@@ -950,3 +950,29 @@ def test_sdpa_flash_head_sizes_32_96_mask_and_layout(cuda, nat, oracle, D):
     qh, kh, vh = (host(t).transpose(0, 2, 1, 3) for t in (q, k, v))
     ref = oracle.sdpa(qh, kh, vh, 0.2, mask=mask).transpose(0, 2, 1, 3)
     check_sdpa(out, ref, "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [32, 96])
+@pytest.mark.parametrize("hq,hkv,tq,tk", [(32, 1, 1, 64), (16, 2, 4, 1000), (8, 8, 1, 4097), (4, 2, 1, 1)])
+def test_sdpa_decode_mfma_head_sizes_32_96(cuda, nat, oracle, dtype, D, hq, hkv, tq, tk):
+    """The MFMA split-KV decode at head sizes 32 and 96 (64- / 128-wide LDS
+    tiles, the head's features only in the MFMAs; the combine's lanes cover
+    the head's features): ragged tiles and splits, GQA, causal, a padding
+    mask and a fused q RMSNorm with weight."""
+    td = cuda.bfloat16 if dtype == "bf16" else cuda.float16
+    tol = BF16_REL_TOL if dtype == "bf16" else 5e-3
+    q, k, v = make_qkv(cuda, 73, (2, hq, tq, D), (2, hkv, tk, D), td)
+    assert nat.sdpa_kernel_name(q, k, v) == "decode_splitkv_mfma"
+    out = nat.sdpa(q, k, v, scale=D ** -0.5)
+    assert rel_inf(host(out), oracle.sdpa(host(q), host(k), host(v), D ** -0.5)) <= tol
+    out_c = nat.sdpa(q, k, v, scale=D ** -0.5, causal=True)
+    assert rel_inf(host(out_c), oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=True)) <= tol
+    lens = np.array([tk, max(1, tk // 3)])
+    mask = np.where(np.arange(tk)[None] < lens[:, None], 0.0, -np.inf).reshape(2, 1, 1, tk)
+    maskd = dev(cuda, mask, cuda.float32)
+    w = dev(cuda, 1 + 0.1 * np.random.default_rng(74).standard_normal(D), td)
+    out_m = nat.sdpa(q, k, v, scale=0.1, mask=maskd, q_rms_eps=1e-6, q_rms_weight=w)
+    qn = oracle.rms_norm(host(q), host(w), 1e-6)
+    qn = host(cuda.from_numpy(qn.astype(np.float32)).to(td))
+    assert rel_inf(host(out_m), oracle.sdpa(qn, host(k), host(v), 0.1, mask=mask)) <= tol
