@@ -181,6 +181,31 @@ def bench_masked_prefill(torch, native, steps, warmup):
     return res
 
 
+def bench_head_sizes(torch, native, steps, warmup):
+    """Causal prefill [B=4, H=32, T=2048, d] per head size d in 32, 64, 96,
+    128: bf16 and f16 (the pipelined flash kernel), and f32 (the f32 flash
+    kernel) at T=1024.  TFLOP/s on the causal count 4*B*H*d*T(T+1)/2."""
+    import numpy as np
+
+    res = []
+    for dt, T in (("bf16", 2048), ("f16", 2048), ("f32", 1024)):
+        tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dt]
+        for d in (32, 64, 96, 128):
+            B, H = 4, 32
+            rng = np.random.default_rng(3)
+            q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32)).to("cuda").to(tdt)
+                       for _ in range(3))
+            out = torch.empty_like(q)
+            avg_ms, med_ms, _ = time_launches(
+                torch, lambda: native.sdpa(q, k, v, scale=d ** -0.5, causal=True, out=out), steps, warmup)
+            flops = sdpa_causal_flops(B, H, T, d)
+            res.append({"dtype": dt, "shape": [B, H, T, d], "avg_us": round(avg_ms * 1e3, 2),
+                        "median_us": round(med_ms * 1e3, 2), "TFLOPs": round(flops / (avg_ms * 1e-3) / 1e12, 1),
+                        "kernel": native.sdpa_kernel_name(q, k, v, causal=True)})
+            del q, k, v, out
+    return {"causal_prefill": res}
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -592,6 +617,7 @@ ONLY = {
                   bench_layer_norm(torch, native, 65536, 4096, k, w)]},
     "copy": lambda torch, native, k, w: bench_copy(torch, k, w),
     "masked_prefill": lambda torch, native, k, w: bench_masked_prefill(torch, native, k, w),
+    "head_sizes": lambda torch, native, k, w: bench_head_sizes(torch, native, k, w),
     "pjrt": lambda torch, native, k, w: {
         "config3_pjrt": bench_sdpa_pjrt(torch, 3, k, w, bench_config3(torch, native, k, w)["avg_ms"] * 1e3),
         "config5_pjrt": bench_sdpa_pjrt(torch, 5, k, w, bench_config5(torch, native, k, w)["avg_us"])},
@@ -692,6 +718,9 @@ def main() -> int:
         extra["config2_sdpa_f32"] = bench_config2(torch, native, 200, 20)
         log("masked prefill: padding mask [4,1,1,2048] on [4,32,2048,128] bf16")
         extra["masked_prefill"] = bench_masked_prefill(torch, native, 20, 3)
+        torch.cuda.empty_cache()
+        log("head sizes 32 / 64 / 96 / 128: causal prefill, bf16, f16, f32")
+        extra["head_sizes"] = bench_head_sizes(torch, native, 10, 2)
         torch.cuda.empty_cache()
         log("config 5: GQA decode bf16 + RMSNorm(q)")
         extra["config5_decode"] = bench_config5(torch, native, 50, 5)

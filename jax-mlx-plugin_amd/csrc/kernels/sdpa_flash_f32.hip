@@ -66,10 +66,10 @@ struct Cfg {
   static constexpr int CH = KS * DCH / kNT;        // chunks per thread per stage
 };
 
-// Two workgroups per CU (256 VGPRs) except masked D = 128, whose extra mask
-// state would spill at that bound.
+// Two workgroups per CU (256 VGPRs) except masked D = 96 and 128, whose
+// extra mask state would spill at that bound.
 template <int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kNT, (D == 128 && MASK) ? 1 : 2) void flash_f32_kernel(SdpaParams p) {
+__global__ __launch_bounds__(kNT, (D >= 96 && MASK) ? 1 : 2) void flash_f32_kernel(SdpaParams p) {
   using C = Cfg<D, MASK>;
   __shared__ __attribute__((aligned(16))) float k_lds[2][C::KS * C::KROW];
   __shared__ __attribute__((aligned(16))) float v_lds[2][C::KS * C::VROW];
@@ -546,7 +546,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 bool flash_f32_supports(const SdpaParams& p) {
   if (p.dtype != MFX_F32) return false;
-  if (p.D != p.Dv || (p.D != 64 && p.D != 128)) return false;
+  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 4 || p.ks[i] % 4 || p.vs[i] % 4 || p.os[i] % 4) return false;
@@ -558,8 +558,12 @@ bool flash_f32_supports(const SdpaParams& p) {
 }
 
 int launch_flash_f32(const SdpaParams& p, hipStream_t s) {
-  if (p.D == 128) return launch_d<128>(p, s);
-  return launch_d<64>(p, s);
+  switch (p.D) {
+    case 32: return launch_d<32>(p, s);
+    case 96: return launch_d<96>(p, s);
+    case 128: return launch_d<128>(p, s);
+    default: return launch_d<64>(p, s);
+  }
 }
 
 }  // namespace mfx

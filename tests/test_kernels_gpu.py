@@ -976,3 +976,24 @@ def test_sdpa_decode_mfma_head_sizes_32_96(cuda, nat, oracle, dtype, D, hq, hkv,
     qn = oracle.rms_norm(host(q), host(w), 1e-6)
     qn = host(cuda.from_numpy(qn.astype(np.float32)).to(td))
     assert rel_inf(host(out_m), oracle.sdpa(qn, host(k), host(v), 0.1, mask=mask)) <= tol
+
+
+@pytest.mark.parametrize("D", [32, 96])
+@pytest.mark.parametrize("tq,tk,hq,hkv,causal,masked", [(128, 128, 8, 8, False, False), (100, 77, 4, 2, True, False),
+                                                        (33, 300, 4, 1, False, True), (77, 200, 2, 2, True, True),
+                                                        (1000, 1000, 1, 1, True, False)])
+def test_sdpa_f32_head_sizes_32_96(cuda, nat, oracle, D, tq, tk, hq, hkv, causal, masked):
+    """The f32 flash kernels (row-block and key-split) at head sizes 32 and
+    96: ragged, GQA, causal, an additive mask with -inf holes."""
+    q, k, v = make_qkv(cuda, 75, (2, hq, tq, D), (2, hkv, tk, D), cuda.float32)
+    mask = None
+    if masked:
+        m = np.random.default_rng(76).standard_normal((2, 1, tq, tk)) * 0.5
+        m[..., ::5] = -np.inf
+        m[..., 0] = 0.0
+        mask = m
+    maskd = None if mask is None else dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, causal=causal, mask=maskd).startswith("flash_f32")
+    assert nat.sdpa_kernel_name(q, k, v, causal=causal, mask=maskd).endswith(f"_d{D}")
+    out = nat.sdpa(q, k, v, scale=D ** -0.5, causal=causal, mask=maskd)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=causal, mask=mask), "f32")
