@@ -99,7 +99,9 @@ def graph_replay_us(torch, fn, reps: int = 100):
             fn()
         torch.cuda.current_stream().wait_stream(stream)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        # Captured on the stream the warm-up call ran on: library scratch is
+        # per stream and grows (allocates) only outside the capture.
+        with torch.cuda.graph(graph, stream=stream):
             for _ in range(reps):
                 fn()
         graph.replay()
@@ -540,6 +542,44 @@ def bench_config4_gemms(torch, native, steps, warmup):
     return out
 
 
+def bench_gemm16(torch, native, steps, warmup):
+    """bf16 GEMMs of one transformer training step at config 4's widths
+    (B*T = 8192 rows, d 512, MLP 2048, QKV 1536), on the hand-written 16-bit
+    tile kernel (mfx_gemm, gemm16.hip) beside torch.matmul (hipBLASLt) of the
+    same product: the forward x W, the weight gradient x^T dy (A transposed)
+    and the input gradient dy W^T (B transposed).  bf16 in and out, fp32
+    accumulation; inputs from default_rng(6).  Device time per call from
+    graph replay."""
+    import numpy as np
+
+    rng = np.random.default_rng(6)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda().bfloat16()  # noqa: E731
+    out = {}
+    R = 8192
+    for label, m, n, k, ta, tb in (("fwd_qkv x W", R, 1536, 512, False, False),
+                                   ("fwd_mlp_in x W", R, 2048, 512, False, False),
+                                   ("fwd_mlp_out x W", R, 512, 2048, False, False),
+                                   ("dW_mlp_in x^T dy", 512, 2048, R, True, False),
+                                   ("dx_mlp_in dy W^T", R, 512, 2048, False, True)):
+        a = dev(rng.standard_normal((k, m) if ta else (m, k)))
+        b = dev(rng.standard_normal((n, k) if tb else (k, n)) / np.sqrt(k))
+        c = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+        opa = a.t() if ta else a
+        opb = b.t() if tb else b
+        fns = {"tile_gemm": lambda: native.gemm(a, b, c, trans_a=ta, trans_b=tb),
+               "torch_matmul": lambda: torch.matmul(opa, opb)}
+        flops = 2.0 * m * n * k
+        res = {"shape_mnk": [m, n, k], "trans_a": ta, "trans_b": tb,
+               "kernel": native.gemm_kernel_name(a, b, c, ta, tb)}
+        for key, fn in fns.items():
+            avg_ms, _, _ = time_launches(torch, fn, steps, warmup)
+            g_us = graph_replay_us(torch, fn, reps=20)
+            res[key] = {"eager_us": round(avg_ms * 1e3, 2), "device_us": round(g_us, 2) if g_us else None,
+                        "TFLOPs": round(flops / ((g_us or avg_ms * 1e3) * 1e-6) / 1e12, 1)}
+        out[label] = res
+    return out
+
+
 def bench_config3_bwd(torch, native, steps, warmup):
     """mfx_sdpa_bwd on the config-3 shape (causal bf16 [4,32,2048,128]) two
     ways.  As the custom_call @mlx_sdpa_bwd interface runs it (q, k, v and
@@ -611,6 +651,7 @@ ONLY = {
     "config3": lambda torch, native, k, w: bench_config3(torch, native, k, w),
     "config4": lambda torch, native, k, w: bench_config4(torch, k, w),
     "config4_gemm": lambda torch, native, k, w: bench_config4_gemms(torch, native, k, w),
+    "gemm16": lambda torch, native, k, w: bench_gemm16(torch, native, k, w),
     "config5": lambda torch, native, k, w: bench_config5(torch, native, k, w),
     "ln_sweep": lambda torch, native, k, w: {
         "sweep": [bench_layer_norm(torch, native, 1 << 20, 512, k, w),
@@ -744,6 +785,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("config 4 dense layers: fused tile GEMM vs plain tile GEMM vs torch.matmul")
         extra["config4_gemms"] = bench_config4_gemms(torch, native, 20, 3)
+        torch.cuda.empty_cache()
+        log("bf16 GEMMs of a training step: 16-bit tile kernel vs torch.matmul")
+        extra["gemm16_training_step"] = bench_gemm16(torch, native, 20, 3)
         torch.cuda.empty_cache()
         line["extra"] = extra
 

@@ -461,8 +461,17 @@ int mfx_reduce(const mfx_reduce_args* args, void* stream);
  * B_i at b + i*stride_b stored [k][n] (ldb) or, if trans_b, [n][k].
  * fp32 accumulation; a/b share `dtype`, c has `c_dtype`.  f32 products
  * without transposes whose A and B rows are 16-byte aligned (k % 4 == 0,
- * lda and ldb multiples of 4, even n) run on the hand-written MFMA tile
- * kernel; every other case on rocBLAS (mfx_gemm_kernel_name tells which).
+ * lda and ldb multiples of 4, even n) run on the hand-written f32 MFMA tile
+ * kernel; bf16 / f16 products in any transpose combination (k % 8 == 0,
+ * n % 4 == 0, A and B 16-byte aligned with lda, ldb and batch strides
+ * multiples of 8, c rows 4-element aligned) on the hand-written 16-bit MFMA
+ * tile kernel; every other case on rocBLAS (mfx_gemm_kernel_name tells
+ * which).  The 16-bit kernel splits K over workgroups when the output tiles
+ * are too few to fill the device (a weight gradient x^T dy): fp32 partials in
+ * the library's scratch for the call's stream, summed in a fixed order (the
+ * result is deterministic).  That scratch is allocated on first use per
+ * stream and size: a call captured into a graph needs an eager call of the
+ * same or a larger split size on the capturing stream first.
  * Replaces the dot_general lowering (reference src/jax_mlx_pjrt.cpp:4577-4666). */
 typedef struct {
   const void* a;
@@ -480,8 +489,9 @@ typedef struct {
 int mfx_gemm(const mfx_gemm_args* args, void* stream);
 
 /* Name of the kernel mfx_gemm runs for args (no device needed; pointers are
- * read for their alignment): "gemm_f32_tile" (hand-written MFMA kernel) or
- * "rocblas".  For tests and traces. */
+ * read for their alignment): "gemm_f32_tile", "gemm_bf16_tile",
+ * "gemm_f16_tile" (hand-written MFMA kernels) or "rocblas".  For tests and
+ * traces. */
 const char* mfx_gemm_kernel_name(const mfx_gemm_args* args);
 
 /* GEMM with a fused elementwise epilogue: out = epi(inputs) where epi's

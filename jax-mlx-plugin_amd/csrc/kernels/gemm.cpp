@@ -1,16 +1,18 @@
 // mfx_gemm: batched strided GEMM for the dot_general ops.
 //
 // f32 row-major products without transposes (the dense layers of a
-// transformer) run on the hand-written MFMA tile kernel (gemm_f32.hip);
-// every other case goes to rocBLAS's gemm_strided_batched_ex with fp32
-// accumulation, issuing row-major C = op(A) op(B) as the column-major
-// product C^T = op(B)^T op(A)^T.
+// transformer) run on the hand-written f32 MFMA tile kernel (gemm_f32.hip),
+// bf16 / f16 products in any transpose combination on the 16-bit one
+// (gemm16.hip); every other case goes to rocBLAS's gemm_strided_batched_ex
+// with fp32 accumulation, issuing row-major C = op(A) op(B) as the
+// column-major product C^T = op(B)^T op(A)^T.
 #include <rocblas/rocblas.h>
 
 #include <mutex>
 #include <vector>
 
 #include "common.h"
+#include "gemm16.h"
 #include "gemm_f32.h"
 
 namespace mfx {
@@ -63,6 +65,7 @@ extern "C" int mfx_gemm(const mfx_gemm_args* a, void* stream) {
   if (a->lda < a_cols || a->ldb < b_cols || a->ldc < a->n)
     return fail(MFX_E_INVALID, "gemm leading dimension too small");
   if (gemm_f32_supported(*a)) return gemm_f32_launch(*a, static_cast<hipStream_t>(stream));
+  if (gemm16_supported(*a)) return gemm16_launch(*a, static_cast<hipStream_t>(stream));
   rocblas_handle h;
   int rc = handle_for_current_device(&h);
   if (rc != MFX_OK) return rc;
@@ -91,5 +94,7 @@ extern "C" int mfx_gemm(const mfx_gemm_args* a, void* stream) {
 
 extern "C" const char* mfx_gemm_kernel_name(const mfx_gemm_args* a) {
   if (!a) return "invalid";
-  return mfx::gemm_f32_supported(*a) ? "gemm_f32_tile" : "rocblas";
+  if (mfx::gemm_f32_supported(*a)) return "gemm_f32_tile";
+  if (mfx::gemm16_supported(*a)) return a->dtype == MFX_F16 ? "gemm_f16_tile" : "gemm_bf16_tile";
+  return "rocblas";
 }

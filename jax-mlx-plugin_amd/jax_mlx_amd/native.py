@@ -600,14 +600,18 @@ def _matrix(x):
     return x.shape[0], x.shape[1], x.shape[2], x.stride(1), x.stride(0)
 
 
-def gemm_args(a, b, c=None):
-    """GemmArgs for c = a @ b (row-major, optionally batched; b may be 2-D
-    and shared by every batch of a)."""
-    ba, m, k, lda, sa = _matrix(a)
-    bb, k2, n, ldb, sb = _matrix(b)
+def gemm_args(a, b, c=None, trans_a=False, trans_b=False):
+    """GemmArgs for c = op(a) @ op(b) (row-major, optionally batched; b may
+    be 2-D and shared by every batch of a).  trans_a: a is stored [k, m];
+    trans_b: b is stored [n, k]."""
+    ba, r, s_, lda, sa = _matrix(a)
+    m, k = (s_, r) if trans_a else (r, s_)
+    bb, r2, s2, ldb, sb = _matrix(b)
+    k2, n = (s2, r2) if trans_b else (r2, s2)
     if k2 != k or (bb != ba and bb != 1):
         raise ValueError("GEMM extents disagree")
     g = GemmArgs()
+    g.trans_a, g.trans_b = int(trans_a), int(trans_b)
     g.a, g.b = a.data_ptr(), b.data_ptr()
     g.c = c.data_ptr() if c is not None else None
     g.dtype = dtype_code(a.dtype)
@@ -618,23 +622,27 @@ def gemm_args(a, b, c=None):
     return g
 
 
-def gemm(a, b, out=None):
-    """mfx_gemm: a [(batch,) m, k] @ b [(batch,) k, n] into a new contiguous
-    f32 tensor (or `out`)."""
+def gemm(a, b, out=None, trans_a=False, trans_b=False, out_dtype=None):
+    """mfx_gemm: op(a) [(batch,) m, k] @ op(b) [(batch,) k, n] into a new
+    contiguous tensor of out_dtype (default f32), or `out`.  trans_a: a is
+    stored [(batch,) k, m]; trans_b: b is stored [(batch,) n, k]."""
     torch = _torch()
     _require_gpu(a, b)
     batch = a.shape[0] if a.dim() == 3 else None
-    shape = (batch, a.shape[-2], b.shape[-1]) if batch is not None else (a.shape[-2], b.shape[-1])
+    m = a.shape[-1] if trans_a else a.shape[-2]
+    n = b.shape[-2] if trans_b else b.shape[-1]
+    shape = (batch, m, n) if batch is not None else (m, n)
     if out is None:
-        out = torch.empty(shape, dtype=torch.float32, device=a.device)
-    g = gemm_args(a, b, out)
+        out = torch.empty(shape, dtype=out_dtype or torch.float32, device=a.device)
+    g = gemm_args(a, b, out, trans_a, trans_b)
     check(load().mfx_gemm(ctypes.byref(g), _stream_handle(a)))
     return out
 
 
-def gemm_kernel_name(a, b, out=None) -> str:
-    """Kernel mfx_gemm runs for a @ b: "gemm_f32_tile" or "rocblas"."""
-    return load().mfx_gemm_kernel_name(ctypes.byref(gemm_args(a, b, out))).decode()
+def gemm_kernel_name(a, b, out=None, trans_a=False, trans_b=False) -> str:
+    """Kernel mfx_gemm runs for op(a) @ op(b): "gemm_f32_tile",
+    "gemm_bf16_tile", "gemm_f16_tile" or "rocblas"."""
+    return load().mfx_gemm_kernel_name(ctypes.byref(gemm_args(a, b, out, trans_a, trans_b))).decode()
 
 
 def _bind_inputs(prog, tensors):
