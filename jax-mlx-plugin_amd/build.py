@@ -99,17 +99,162 @@ def _check_no_spill(src: Path, remarks: str) -> None:
         raise RuntimeError(f"{src.name}: VGPR spills in a kernel with inline-asm LDS reads:\n" + "\n".join(bad))
 
 
+# LDS-wait check of the same kernels, on their gfx950 assembly (built here
+# from source): the compiler's wait insertion does not see loads issued from
+# inline asm, so nothing but the code's own lgkmcnt waits keeps a later
+# instruction from reading (or a VALU write from clobbering) an LDS read's
+# destination before the data arrives.  Per kernel, a dataflow over the basic
+# blocks tracks the LDS / scalar-memory operations in flight: LDS operations
+# complete in issue order, scalar loads in any order, so `s_waitcnt
+# lgkmcnt(N)` is taken to retire the scalar loads first and then the oldest
+# LDS operations until N remain.  At a block with
+# several predecessors the in-flight lists are aligned from the newest and
+# merged register by register.  Any access to a register an LDS read still
+# owes is an error, except a later LDS read into it (it completes after).
+_VREG = re.compile(r"\b([va])(?:(\d+)|\[(\d+):(\d+)\])")
+_LGKM_MAX = 15
+_LGKM_SMEM = ("s_load", "s_buffer_load", "s_memtime", "s_memrealtime", "s_sendmsg")
+
+
+def _vregs(text: str) -> set:
+    out = set()
+    for m in _VREG.finditer(text):
+        if m.group(2) is not None:
+            out.add((m.group(1), int(m.group(2))))
+        else:
+            out.update((m.group(1), r) for r in range(int(m.group(3)), int(m.group(4)) + 1))
+    return out
+
+
+def _lgkm_wait(ins: str):
+    m = re.search(r"lgkmcnt\((\d+)\)", ins)
+    if m:
+        return int(m.group(1))
+    m = re.match(r"s_waitcnt\s+(0x[0-9a-fA-F]+|\d+)\s*$", ins)
+    if m:
+        c = (int(m.group(1), 0) >> 8) & 0xF
+        return None if c == 0xF else c
+    return None
+
+
+def _retire(fl: list, keep: int) -> None:
+    # what `s_waitcnt lgkmcnt(keep)` guarantees (and what the 4-bit counter
+    # forces before an issue past 15 in flight): scalar loads retire first,
+    # then LDS operations oldest first
+    while len(fl) > keep:
+        fl.pop(next((j for j, e in enumerate(fl) if e[0] and not e[1]), 0))
+
+
+def _merge_inflight(a: tuple, b: tuple) -> tuple:
+    n = max(len(a), len(b))
+    pad = ((False, frozenset()),)
+    a = pad * (n - len(a)) + a
+    b = pad * (n - len(b)) + b
+    return tuple((x[0] or y[0], x[1] | y[1]) for x, y in zip(a, b))
+
+
+def _lds_wait_errors(lines: list) -> list:
+    blocks = [[None, []]]
+    for ln, text in lines:
+        code = text.split(";")[0].rstrip()
+        if not code.strip():
+            continue
+        m = re.match(r"^(\.LBB\d+_\d+):", code)
+        if m:
+            blocks.append([m.group(1), []])
+            continue
+        ins = code.strip()
+        if not ins.startswith("."):
+            blocks[-1][1].append((ln, ins))
+    label_of = {b[0]: i for i, b in enumerate(blocks) if b[0]}
+    errors = []
+    state_in = {0: ()}
+    work = [0]
+
+    def reach(j: int, state: tuple) -> None:
+        merged = state if j not in state_in else _merge_inflight(state_in[j], state)
+        if state_in.get(j) != merged:
+            state_in[j] = merged
+            work.append(j)
+
+    while work:
+        i = work.pop()
+        fl = list(state_in[i])
+        falls_through = True
+        for ln, ins in blocks[i][1]:
+            mn = ins.split()[0]
+            if mn == "s_waitcnt":
+                w = _lgkm_wait(ins)
+                if w is not None:
+                    _retire(fl, w)
+                continue
+            if mn == "s_branch" or mn.startswith("s_cbranch"):
+                if ins.split()[-1] in label_of:
+                    reach(label_of[ins.split()[-1]], tuple(fl))
+                if mn == "s_branch":
+                    falls_through = False
+                    break
+                continue
+            if mn == "s_endpgm":
+                falls_through = False
+                break
+            owed = set().union(*(e[1] for e in fl)) if fl else set()
+            ops = ins[len(mn):]
+            if mn.startswith("ds_"):
+                parts = ops.split(",")
+                dest_read = any(t in mn for t in ("read", "load", "_rtn", "permute", "swizzle", "append", "consume"))
+                dest = _vregs(parts[0]) if dest_read else set()
+                src = _vregs(",".join(parts[1:])) if dest_read else _vregs(ops)
+                if src & owed:
+                    errors.append(f"line {ln}: {ins}")
+                _retire(fl, _LGKM_MAX - 1)
+                fl.append((False, frozenset(dest)))
+            elif mn.startswith(_LGKM_SMEM):
+                _retire(fl, _LGKM_MAX - 1)
+                fl.append((True, frozenset()))
+            elif _vregs(ops) & owed:
+                errors.append(f"line {ln}: {ins}")
+        if falls_through and i + 1 < len(blocks):
+            reach(i + 1, tuple(fl))
+    return sorted(set(errors), key=lambda e: int(e.split()[1].rstrip(":")))
+
+
+def _check_lds_waits(src: Path, asm: str) -> None:
+    bad = []
+    name, body = None, []
+    for ln, text in enumerate(asm.splitlines(), 1):
+        m = re.match(r"^(_Z\S+):", text)
+        if m:
+            name, body = m.group(1), []
+            continue
+        if name and text.startswith(".Lfunc_end"):
+            bad += [f"{name}: {e}" for e in _lds_wait_errors(body)]
+            name = None
+        elif name:
+            body.append((ln, text))
+    if bad:
+        raise RuntimeError(f"{src.name}: registers read before their LDS data arrives:\n" + "\n".join(bad[:20]))
+
+
 def _compile_hip(src: Path, obj: Path) -> Path:
     cmd = [HIPCC, *HIP_FLAGS, f"-I{obj.parent}", *HIP_FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.name not in NO_SPILL_FILES:
         _run(cmd)
         return obj
+    asm = obj.with_suffix(".s")
+    asm_cmd = [HIPCC, *HIP_FLAGS, f"-I{obj.parent}", *HIP_FILE_FLAGS.get(src.name, []), "--cuda-device-only", "-S",
+               str(src), "-o", str(asm)]
+    asm_proc = subprocess.Popen(asm_cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     proc = subprocess.run([*cmd, _RESOURCE_REMARK], capture_output=True, text=True)
+    asm_out = asm_proc.communicate()[0]
     out = proc.stdout + proc.stderr
     if proc.returncode != 0:
         lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l and "remark:" not in l]
         raise RuntimeError("command failed: " + " ".join(cmd) + "\n" + "\n".join(lines))
     _check_no_spill(src, out)
+    if asm_proc.returncode != 0:
+        raise RuntimeError("command failed: " + " ".join(asm_cmd) + "\n" + asm_out)
+    _check_lds_waits(src, asm.read_text())
     return obj
 
 
