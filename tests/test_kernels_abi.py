@@ -201,19 +201,32 @@ def test_calls_fail_loudly_without_a_gpu(native):
 # ---------------------------------------------------------------- GEMM
 
 def test_gemm_kernel_selection(native):
-    """f32 row-major products go to the hand-written MFMA tile kernel; what it
-    does not take (bf16, K % 4, odd N, rows not 16-byte aligned) to rocBLAS."""
+    """f32 row-major products without transposes go to the hand-written f32
+    MFMA tile kernel, bf16 / f16 products in any transpose combination to the
+    16-bit one; what neither takes (K % 4 for f32 and K % 8 for 16-bit, odd
+    or N % 4 != 0, rows not 16-byte aligned, transposed f32) to rocBLAS."""
     import torch
 
     f = torch.float32
     a, b = torch.zeros(8192, 512, dtype=f), torch.zeros(512, 1536, dtype=f)
     assert native.gemm_kernel_name(a, b) == "gemm_f32_tile"
     assert native.gemm_kernel_name(torch.zeros(3, 100, 64, dtype=f), torch.zeros(3, 64, 96, dtype=f)) == "gemm_f32_tile"
-    assert native.gemm_kernel_name(a.bfloat16(), b.bfloat16()) == "rocblas"
     assert native.gemm_kernel_name(torch.zeros(64, 6, dtype=f), torch.zeros(6, 64, dtype=f)) == "rocblas"
     assert native.gemm_kernel_name(torch.zeros(64, 8, dtype=f), torch.zeros(8, 63, dtype=f)) == "rocblas"
     flat = torch.zeros(64 * 8 + 1, dtype=f)
     assert native.gemm_kernel_name(flat[1:].view(64, 8), torch.zeros(8, 64, dtype=f)) == "rocblas"
+    assert native.gemm_kernel_name(a.t().contiguous(), b, trans_a=True) == "rocblas"
+    for dt, name in ((torch.bfloat16, "gemm_bf16_tile"), (torch.float16, "gemm_f16_tile")):
+        a16, b16 = a.to(dt), b.to(dt)
+        assert native.gemm_kernel_name(a16, b16) == name
+        assert native.gemm_kernel_name(a16, b16.t().contiguous(), trans_b=True) == name          # x W^T
+        assert native.gemm_kernel_name(a16.t().contiguous(), b16, trans_a=True) == name          # x^T dy
+        assert native.gemm_kernel_name(a16.t().contiguous(), b16.t().contiguous(), trans_a=True,
+                                       trans_b=True) == name
+        assert native.gemm_kernel_name(torch.zeros(64, 36, dtype=dt), torch.zeros(36, 64, dtype=dt)) == "rocblas"
+        assert native.gemm_kernel_name(torch.zeros(64, 32, dtype=dt), torch.zeros(32, 66, dtype=dt)) == "rocblas"
+        flat16 = torch.zeros(64 * 32 + 4, dtype=dt)
+        assert native.gemm_kernel_name(flat16[4:].view(64, 32), torch.zeros(32, 64, dtype=dt)) == "rocblas"
 
 
 def _fused_pair(native, name, dims, K):
