@@ -29,12 +29,49 @@
 // Tiles use the forward kernel's XOR swizzle, so every operand read is bank
 // conflict free; causal tiles that see nothing are skipped, diagonal and
 // ragged tiles mask per element.
+//
+// Built with -DMFX_PHASE_TIMERS (build.py phase_timers, a separate
+// diagnostic library), every wavefront of the dK/dV kernel also records
+// where its time goes: s_memrealtime stamps (100 MHz) at its start, at its
+// loop entry and at its end, and s_memtime (shader clock) sums over its
+// X phases (S / dP MFMAs), its Y | V phases (dV / dK MFMAs with the next
+// block's exp2 / dS work), its barriers (vmcnt wait, s_barrier, the next
+// tile's DMA issue) and its last Y, read where none of its inline-asm LDS
+// reads is outstanding and summed in LDS (its SGPRs are all taken).  mfx_bwd_phase_timers_read() copies the records
+// out; jax-mlx-plugin_amd/phase_budget.py --kernel dkdv turns them into the
+// per-block budget.
 #include <type_traits>
 
 #include "sdpa_elem.h"
 #include "sdpa_tiles.h"
 
+#if defined(MFX_PHASE_TIMERS)
+#define PHASE(...) __VA_ARGS__
+#else
+#define PHASE(...)
+#endif
+
 namespace mfx {
+
+#if defined(MFX_PHASE_TIMERS)
+// One record of kBwdPhaseFields u64 per dK/dV wavefront (blockIdx.x * 4 + wave).
+constexpr int kBwdPhaseRecords = 1 << 15;
+constexpr int kBwdPhaseFields = 16;
+__device__ unsigned long long g_bwd_phase_records[kBwdPhaseRecords * kBwdPhaseFields];
+
+// The kernel's SGPRs are all taken, so the running sums live in LDS: slot f
+// of wavefront w is 64 words (one per lane, all equal), added to with
+// ds_add_u32 at points where none of the kernel's inline-asm LDS reads is
+// outstanding (an older LDS operation still in flight only makes their
+// counted lgkmcnt waits stricter).
+enum BwdPhaseSlot {
+  kPhX, kPhYV, kPhSync, kPhVmwait, kPhBarrier, kPhLast, kPhBlocks, kPhEdges, kPhTiles,
+  kPhRtStart, kPhCStart, kPhRtLoop, kPhCLoop, kPhCEpi, kBwdPhaseSlots
+};
+__device__ __forceinline__ unsigned ph_now() { return (unsigned)__builtin_amdgcn_s_memtime(); }
+__device__ __forceinline__ unsigned ph_real() { return (unsigned)__builtin_amdgcn_s_memrealtime(); }
+#endif
+
 namespace {
 
 constexpr int kNT = 256;  // 4 wavefronts
@@ -126,6 +163,7 @@ __device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int hal
 // and the wavefront with the most visible blocks sets the pace anyway.
 constexpr int kKvPf = 2;   // operand reads issued ahead of their MFMAs
 constexpr int kKvStages = 3;
+constexpr int kDkdvHeadGroup = 2;  // kv heads whose key blocks an XCD runs together
 
 template <int D, bool CAUSAL, bool MASK, int E>
 __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
@@ -137,6 +175,17 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   constexpr int LB = 2 * kKvStages * TB;       // byte offset of the lse / delta rows
   constexpr int LS = 2 * kTile * 4;            // their bytes per stage (lse | delta)
   __shared__ __attribute__((aligned(16))) char smem[LB + kKvStages * LS];
+#if defined(MFX_PHASE_TIMERS)
+  __shared__ unsigned ph_lds[4 * kBwdPhaseSlots * 64];
+  const int ph_lane = threadIdx.x & 63, ph_wave = threadIdx.x >> 6;
+  auto ph_slot = [&](int f) -> unsigned& { return ph_lds[(ph_wave * kBwdPhaseSlots + f) * 64 + ph_lane]; };
+  auto ph_add = [&](int f, unsigned v) {
+    __hip_atomic_fetch_add(&ph_slot(f), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  for (int f = 0; f < kBwdPhaseSlots; ++f) ph_slot(f) = 0;
+  ph_slot(kPhRtStart) = ph_real();
+  ph_slot(kPhCStart) = ph_now();
+#endif
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -145,10 +194,25 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   const int l32 = lane & 31;
 
   const int BHk = p.B * p.Hkv;
-  // Key blocks in ascending order: under a causal mask the first key blocks
-  // see the most queries, so the longest blocks are issued first.
+  const int nkb = (p.Tk + kRows - 1) / kRows;
   const int id = blockIdx.x;
-  const int bhk = id % BHk, kblk = id / BHk;
+  int bhk, kblk;
+  if ((BHk & 7) == 0 && ((BHk >> 3) % kDkdvHeadGroup) == 0) {
+    // Blocks are dealt to the 8 XCDs round-robin.  Each XCD takes its kv
+    // heads in groups whose key blocks all run together (2 heads x 16 key
+    // blocks fill an XCD's 32 CUs at config 3), so the group's Q / dO tiles,
+    // which every key block of a head reads, stay in the XCD's L2.  Key
+    // blocks in ascending order within a group: under a causal mask the
+    // first key blocks see the most queries.
+    const int hg = kDkdvHeadGroup, xcd = id & 7, slot = id >> 3;
+    const int grp = slot / (hg * nkb), r = slot % (hg * nkb);
+    bhk = (grp * hg + r % hg) * 8 + xcd;
+    kblk = r / hg;
+  } else {
+    // Key blocks in ascending order, longest first.
+    bhk = id % BHk;
+    kblk = id / BHk;
+  }
   const int b = bhk / p.Hkv, hk = bhk % p.Hkv;
   const int Tq = p.Tq, Tk = p.Tk, G = p.group;
   const int kw = kblk * kRows + wave * 32;  // this wave's first key
@@ -354,21 +418,30 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   auto step = [&](int t, auto ps_tag, auto pm_tag, auto st_tag, auto mt_tag) __attribute__((always_inline)) {
     constexpr int MT = decltype(mt_tag)::value;
     const int g = tile_head(t), q0b = tile_q(t) * kTile + MT * 32;
+    PHASE(fence(); const unsigned c0 = ph_now(); fence();)
     X(st_tag, mt_tag);
+    PHASE(fence(); const unsigned c1 = ph_now(); fence();)
     const bool edge = (q0b + 32 > Tq) || (CAUSAL && q0b < kw + 31);
     if (edge)
       YV(ps_tag, pm_tag, st_tag, mt_tag, std::true_type{}, std::true_type{}, q0b, g);
     else
       YV(ps_tag, pm_tag, st_tag, mt_tag, std::false_type{}, std::true_type{}, q0b, g);
+    PHASE(fence(); const unsigned c2 = ph_now(); ph_add(kPhX, c1 - c0); ph_add(kPhYV, c2 - c1);
+          ph_add(kPhBlocks, 1u); ph_add(kPhEdges, edge ? 1u : 0u); fence();)
   };
   // Tile t in stage ST, the previous tile in stage PS.
   auto tile = [&](int t, auto st_tag, auto ps_tag) __attribute__((always_inline)) {
     constexpr int ST = decltype(st_tag)::value;
+    PHASE(fence(); const unsigned c0 = ph_now(); fence();)
     wait_dma();
+    PHASE(fence(); const unsigned cw = ph_now(); fence();)
     __syncthreads();
+    PHASE(fence(); const unsigned cb = ph_now(); fence();)
     // Stage (ST+1) % 3 last held tile t-2, whose last block's Y ran during
     // tile t-1, before this barrier.
     if (t + 1 < ntiles) issue(t + 1, (ST + 1) % kKvStages);
+    PHASE(fence(); const unsigned ci = ph_now(); ph_add(kPhSync, ci - c0); ph_add(kPhVmwait, cw - c0);
+          ph_add(kPhBarrier, cb - cw); ph_add(kPhTiles, 1u); fence();)
     step(t, ps_tag, std::integral_constant<int, 1>{}, st_tag, std::integral_constant<int, 0>{});
     step(t, st_tag, std::integral_constant<int, 0>{}, st_tag, std::integral_constant<int, 1>{});
   };
@@ -376,6 +449,7 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
 
+  PHASE(fence(); ph_slot(kPhRtLoop) = ph_real(); ph_slot(kPhCLoop) = ph_now(); fence();)
   if (ntiles > 0) {
     // The first block's Y is a no-op: zero P / dS against tile 0's rows.
 #pragma unroll
@@ -392,6 +466,7 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
       tile(t + 2, I0{}, I2{});
     }
     // The last block's Y.
+    PHASE(fence(); const unsigned cl = ph_now(); fence();)
     const int ls = (ntiles - 1) % kKvStages;
     if (ls == 0)
       YV(I0{}, I1{}, I0{}, I0{}, std::false_type{}, std::false_type{}, 0, 0);
@@ -399,14 +474,53 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
       YV(I1{}, I1{}, I0{}, I0{}, std::false_type{}, std::false_type{}, 0, 0);
     else
       YV(I2{}, I1{}, I0{}, I0{}, std::false_type{}, std::false_type{}, 0, 0);
+    PHASE(fence(); ph_add(kPhLast, ph_now() - cl); fence();)
   }
 
+  PHASE(fence(); ph_slot(kPhCEpi) = ph_now(); fence();)
   if (key < Tk) {
     bf16* dko = static_cast<bf16*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + (int64_t)key * p.dks[2];
     bf16* dvo = static_cast<bf16*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + (int64_t)key * p.dvs[2];
     store_rowT<D, E>(dko, dk, half, p.scale);
     store_rowT<D, E>(dvo, dv, half, 1.f);
   }
+#if defined(MFX_PHASE_TIMERS)
+  {
+    // Fields: 0 ids (XCC id, HW_ID, (batch*Hkv + kv head), key block), 1 / 2
+    // realtime start / loop entry (low words), 3 realtime end (64 bits), 4-9
+    // cycles of the X phases / Y | V phases / barrier phases (all) / their
+    // vmcnt waits / their s_barrier / the last Y, 10 blocks, 11 blocks with
+    // per-element masking, 12 total cycles, 13 cycles before the loop, 14
+    // cycles of the epilogue, 15 tiles.
+    fence();
+    unsigned xcc, hwid;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+    const unsigned c_end = ph_now();
+    const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
+    const int rec = id * 4 + wave;
+    if (lane == 0 && rec < kBwdPhaseRecords) {
+      unsigned long long* r = g_bwd_phase_records + (size_t)rec * kBwdPhaseFields;
+      r[0] = (unsigned long long)(xcc & 0xff) | ((unsigned long long)hwid << 8) | ((unsigned long long)bhk << 40) |
+             ((unsigned long long)(kblk & 0xff) << 56);
+      r[1] = ph_slot(kPhRtStart);
+      r[2] = ph_slot(kPhRtLoop);
+      r[3] = rt_end;
+      r[4] = ph_slot(kPhX);
+      r[5] = ph_slot(kPhYV);
+      r[6] = ph_slot(kPhSync);
+      r[7] = ph_slot(kPhVmwait);
+      r[8] = ph_slot(kPhBarrier);
+      r[9] = ph_slot(kPhLast);
+      r[10] = ph_slot(kPhBlocks);
+      r[11] = ph_slot(kPhEdges);
+      r[12] = c_end - ph_slot(kPhCStart);
+      r[13] = ph_slot(kPhCLoop) - ph_slot(kPhCStart);
+      r[14] = c_end - ph_slot(kPhCEpi);
+      r[15] = ph_slot(kPhTiles);
+    }
+  }
+#endif
 }
 
 // ----------------------------------------------------------------------- dQ
@@ -699,3 +813,23 @@ int launch_bwd_mfma(const SdpaBwdParams& p, hipStream_t s) {
 }
 
 }  // namespace mfx
+
+#if defined(MFX_PHASE_TIMERS)
+// Diagnostic build only: copies up to max_records dK/dV phase records
+// (kBwdPhaseFields u64 each, fields as written at the end of bwd_dkdv_mfma) to host memory
+// after the device is idle and returns how many the device array holds;
+// clear != 0 zeroes the array afterwards.  Not part of the product's C ABI.
+extern "C" __attribute__((visibility("default"))) int64_t mfx_bwd_phase_timers_read(void* host, int64_t max_records,
+                                                                                    int clear) {
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  void* dev = nullptr;
+  if (hipGetSymbolAddress(&dev, HIP_SYMBOL(mfx::g_bwd_phase_records)) != hipSuccess) return -1;
+  const int64_t n = max_records < mfx::kBwdPhaseRecords ? max_records : mfx::kBwdPhaseRecords;
+  if (host && n > 0 &&
+      hipMemcpy(host, dev, (size_t)n * mfx::kBwdPhaseFields * 8, hipMemcpyDeviceToHost) != hipSuccess)
+    return -1;
+  if (clear && hipMemset(dev, 0, sizeof(mfx::g_bwd_phase_records)) != hipSuccess) return -1;
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  return mfx::kBwdPhaseRecords;
+}
+#endif

@@ -117,21 +117,22 @@ struct TileLoader {
   // pass of a translation unit sees an empty body.
   //
   // The hardware range check covers the per-lane (VGPR) offset only, not the
-  // scalar offset, so each instruction gets a resource whose base is its
-  // first row and whose extent is what remains of the `nbytes` span from
-  // there: rows past the end then read as zeros instead of touching memory
-  // beyond the tensor.
+  // scalar offset, so one resource spans the `nbytes` from `base` and every
+  // offset -- the tile's `soff`, the instruction's row step and the lane's
+  // row and chunk -- goes into the per-lane offset: rows past the end read
+  // as zeros instead of touching memory beyond the span.  (soff + the lane
+  // offsets stay below 2^32: soff is at most a tile past an extent below
+  // 2^31.)  The resource is loop-invariant, so a caller's loop builds it
+  // once; each instruction costs one vector add.
   __device__ __forceinline__ void load_at(uint32_t soff, bf16* lds, int wave) const {
 #if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(base, (short)0, nbytes > 0 ? nbytes : 0, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const uint32_t off = soff + (i / NOFF) * period_bytes;
-      const int64_t rem = (int64_t)nbytes - (int64_t)off;
-      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-          reinterpret_cast<char*>(base) + off, (short)0, rem > 0 ? (int)rem : 0, 0x00020000);
+    for (int i = 0; i < LOADS; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(lds + (NW * i + wave) * 64 * 8), 16,
-                                               voff[i % NOFF], 0, 0, 0);
-    }
+                                               voff[i % NOFF] + soff + (uint32_t)(i / NOFF) * period_bytes, 0,
+                                               0, 0);
 #endif
   }
   __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {

@@ -1,7 +1,9 @@
-"""Per-tile time budget of the pipelined bf16 flash kernel on config 3.
+"""Per-tile time budget of the pipelined bf16 flash kernel on config 3, and
+per-block budget of the SDPA backward's dK/dV kernel on the same shape.
 
     python jax-mlx-plugin_amd/build.py phase_timers
     python jax-mlx-plugin_amd/phase_budget.py [--json out.json]
+    python jax-mlx-plugin_amd/phase_budget.py --kernel dkdv [--json out.json]
 
 Loads the diagnostic copy of libmfx_kernels.so built with -DMFX_PHASE_TIMERS
 (jax_mlx_amd/lib/phase_timers/), runs causal bf16 SDPA on config 3's inputs
@@ -17,7 +19,16 @@ records the kernel writes (sdpa_flash_bf16_pipe.hip, PhaseClock):
 - per-block start (first tiles landed, loop entry), last tile and epilogue;
 - SIMD occupancy over the kernel span and the spread between XCDs.
 
-The instrumented kernel runs a few percent slower than the shipped one (a
+With --kernel dkdv it runs mfx_sdpa_bwd on the same inputs (upstream
+gradient drawn fourth, from the forward's output and lse, as bench.py's
+config3_sdpa_bwd `from_forward`) and reads the records of bwd_dkdv_mfma
+(sdpa_bwd_mfma.hip): cycles per 32-query block and wavefront in its X phase
+(the S and dP MFMAs), its Y | V phase (the previous block's dV and dK MFMAs
+with this block's exp2 / dS work) and its barrier phase (per 64-query tile:
+vmcnt wait, s_barrier, the next tile's DMA issue), against the MFMA floor
+(one wavefront per SIMD, 32 MFMAs per block).
+
+The instrumented kernels run a few percent slower than the shipped ones (a
 handful of s_memtime reads per tile); shares of the budget are what it is for.
 """
 from __future__ import annotations
@@ -37,6 +48,8 @@ MFMA_CYCLES = 32       # v_mfma_f32_32x32x16_bf16 issue-to-issue on one SIMD
 MFMAS_PER_TILE = 32    # per wavefront and 64-key tile at d = 128: 16 for S, 16 for PV
 WAVES_PER_SIMD = 2
 FIELDS = 20             # u64 per wavefront record (PhaseClock, kPhaseFields)
+BWD_FIELDS = 16         # u64 per dK/dV wavefront record (kBwdPhaseFields)
+BWD_MFMAS_PER_BLOCK = 32  # S, dP, dV, dK: 8 each per 32-query block at d = 128
 
 
 def run(steps: int, lib_path: Path = LIB):
@@ -79,6 +92,119 @@ def run(steps: int, lib_path: Path = LIB):
     return rec, avg_us
 
 
+def occupancy(ids: np.ndarray, rt_start: np.ndarray, rt_end: np.ndarray):
+    """Fraction of the span each SIMD holds 0 / 1 / 2 / 3+ wavefronts (from
+    HW_ID's SIMD / CU / SA / SE fields and the XCC id), and each XCD's finish
+    time after the first wavefront's start (us)."""
+    t0 = rt_start.min()
+    xcc = (ids & 0xff).astype(np.int64)
+    hw = ((ids >> 8) & 0xffffffff).astype(np.int64)
+    simd = (xcc << 16) | (((hw >> 13) & 7) << 12) | (((hw >> 12) & 1) << 11) | (((hw >> 8) & 15) << 4) | \
+        ((hw >> 4) & 3)
+    occ = np.zeros(4)
+    for key in np.unique(simd):
+        m = simd == key
+        ev = sorted([(int(s), 1) for s in rt_start[m]] + [(int(e), -1) for e in rt_end[m]])
+        cur, last = 0, int(t0)
+        for tm, dlt in ev:
+            occ[min(cur, 3)] += tm - last
+            cur += dlt
+            last = tm
+        occ[0] += int(rt_end.max()) - last
+    occ /= occ.sum()
+    xcd_end = {int(x): (rt_end[xcc == x].max() - t0) / RT_HZ * 1e6 for x in np.unique(xcc)}
+    return occ, xcd_end
+
+
+def run_dkdv(steps: int, lib_path: Path = LIB):
+    import ctypes
+
+    import torch
+
+    sys.path.insert(0, str(PKG))
+    from jax_mlx_amd import native
+
+    lib = native.load(lib_path, make_default=True)
+    lib.mfx_bwd_phase_timers_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    lib.mfx_bwd_phase_timers_read.restype = ctypes.c_int64
+    B, H, T, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(3)
+    q, k, v, g = (torch.from_numpy(rng.standard_normal((B, H, T, d)).astype(np.float32)).cuda().bfloat16()
+                  for _ in range(4))
+    lse = torch.empty(B * H * T, dtype=torch.float32, device="cuda")
+    out = native.sdpa(q, k, v, causal=True, lse=lse)
+    ws = torch.empty(native.sdpa_bwd_workspace_size(q, k, v, causal=True, fwd_out=out, fwd_lse=lse),
+                     dtype=torch.uint8, device="cuda")
+    call = lambda: native.sdpa_bwd(q, k, v, g, causal=True, workspace=ws, fwd_out=out, fwd_lse=lse)  # noqa: E731
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.25:
+        call()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    avg_us = e0.elapsed_time(e1) * 1e3 / steps
+    cap = lib.mfx_bwd_phase_timers_read(None, 0, 1)   # clear
+    call()
+    n = B * H * (T // 128) * 4
+    rec = np.zeros((n, BWD_FIELDS), dtype=np.uint64)
+    got = lib.mfx_bwd_phase_timers_read(rec.ctypes.data, n, 0)
+    if got < 0 or cap < n:
+        raise RuntimeError("reading the phase records failed")
+    return rec, avg_us
+
+
+def budget_dkdv(rec: np.ndarray, avg_us: float) -> dict:
+    rec = rec[rec[:, 3] != 0]
+    if not len(rec):
+        raise RuntimeError("no phase records written: the kernel that ran was not the phase-timer build")
+    ids, rt_end = rec[:, 0], rec[:, 3].astype(np.int64)
+    lo = lambda f: ((rec[:, 3] & 0xffffffff).astype(np.int64) - rec[:, f].astype(np.int64)) % (1 << 32)  # noqa
+    rt_start = rt_end - lo(1)
+    rt_loop = rt_end - lo(2)
+    cyc = {name: rec[:, f].astype(np.float64) for name, f in
+           (("X", 4), ("YV", 5), ("S", 6), ("S_vmwait", 7), ("S_barrier", 8), ("last", 9), ("total", 12),
+            ("pre", 13), ("epi", 14))}
+    blocks, edges, tiles = (rec[:, f].astype(np.float64) for f in (10, 11, 15))
+    dur_s = (rt_end - rt_start) / RT_HZ
+    clock_mhz = np.median(cyc["total"] / dur_s) / 1e6
+    t0 = rt_start.min()
+    span_us = (rt_end.max() - t0) / RT_HZ * 1e6
+    nb = blocks.sum()
+    per_block = {p: float(cyc[p].sum() / nb) for p in ("X", "YV", "S")}
+    loop_block = sum(per_block.values())
+    floor = BWD_MFMAS_PER_BLOCK * MFMA_CYCLES
+    occ, xcd_end = occupancy(ids, rt_start, rt_end)
+    us = lambda a: float(np.median(a) / RT_HZ * 1e6)  # noqa: E731
+    return {
+        "kernel": "bwd_dkdv_mfma<128, causal>",
+        "mfx_sdpa_bwd_avg_us_instrumented": round(avg_us, 2),
+        "dkdv_span_us": round(span_us, 2),
+        "shader_clock_mhz": round(float(clock_mhz), 1),
+        "wavefronts": int(len(rec)), "blocks": int(nb), "masked_blocks": int(edges.sum()), "tiles": int(tiles.sum()),
+        "cycles_per_block_per_wavefront": {**{k: round(v, 1) for k, v in per_block.items()},
+                                           "sum": round(loop_block, 1)},
+        "barrier_phase_split_per_block": {
+            "vmcnt_wait": round(float(cyc["S_vmwait"].sum() / nb), 1),
+            "s_barrier": round(float(cyc["S_barrier"].sum() / nb), 1),
+            "dma_issue": round(float((cyc["S"] - cyc["S_vmwait"] - cyc["S_barrier"]).sum() / nb), 1),
+            "note": "one barrier per 64-query tile (two blocks)"},
+        "mfma_floor_cycles_per_block_per_simd": floor,
+        "loop_mfma_fraction": round(floor / loop_block, 4),
+        "median_us_start_to_loop": round(us(rt_loop - rt_start), 3),
+        "median_cycles_last_y": float(np.median(cyc["last"])),
+        "median_cycles_epilogue": float(np.median(cyc["epi"])),
+        "simd_occupancy_fraction_0_1_2_3plus_waves": [round(float(x), 4) for x in occ],
+        "xcd_finish_us": {k: round(v, 2) for k, v in sorted(xcd_end.items())},
+        "xcd_finish_spread_us": round(max(xcd_end.values()) - min(xcd_end.values()), 2),
+        "share_of_wavefront_cycles": {
+            p: round(float(cyc[p].sum() / cyc["total"].sum()), 4) for p in ("pre", "X", "YV", "S", "last", "epi")},
+    }
+
+
 def budget(rec: np.ndarray, avg_us: float) -> dict:
     rec = rec[rec[:, 4] != 0]
     if not len(rec):
@@ -100,23 +226,7 @@ def budget(rec: np.ndarray, avg_us: float) -> dict:
     per_tile = {p: float(cyc[p].sum() / tiles.sum()) for p in ("A", "C", "B", "S")}
     loop_tile = sum(per_tile.values())
     floor = MFMAS_PER_TILE * MFMA_CYCLES * WAVES_PER_SIMD
-    # SIMD occupancy: waves resident per SIMD over the kernel span.
-    xcc = (ids & 0xff).astype(np.int64)
-    hw = ((ids >> 8) & 0xffffffff).astype(np.int64)
-    simd = (xcc << 16) | (((hw >> 13) & 7) << 12) | (((hw >> 12) & 1) << 11) | (((hw >> 8) & 15) << 4) | \
-        ((hw >> 4) & 3)
-    occ = np.zeros(4)
-    for key in np.unique(simd):
-        m = simd == key
-        ev = sorted([(int(s), 1) for s in rt_start[m]] + [(int(e), -1) for e in rt_end[m]])
-        cur, last = 0, int(t0)
-        for tm, dlt in ev:
-            occ[min(cur, 3)] += tm - last
-            cur += dlt
-            last = tm
-        occ[0] += int(rt_end.max()) - last
-    occ /= occ.sum()
-    xcd_end = {int(x): (rt_end[xcc == x].max() - t0) / RT_HZ * 1e6 for x in np.unique(xcc)}
+    occ, xcd_end = occupancy(ids, rt_start, rt_end)
     us = lambda a: float(np.median(a) / RT_HZ * 1e6)  # noqa: E731
     return {
         "kernel_avg_us_instrumented": round(avg_us, 2),
@@ -153,12 +263,18 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--json", help="also write the budget here")
     ap.add_argument("--lib", type=Path, default=LIB, help="a phase-timer build of libmfx_kernels.so")
+    ap.add_argument("--kernel", choices=("flash", "dkdv"), default="flash",
+                    help="flash: the config-3 forward; dkdv: the backward's dK/dV kernel on the same shape")
     args = ap.parse_args()
     if not args.lib.exists():
         print(f"{args.lib} is not built: python jax-mlx-plugin_amd/build.py phase_timers", file=sys.stderr)
         return 1
-    rec, avg_us = run(args.steps, args.lib)
-    b = budget(rec, avg_us)
+    if args.kernel == "dkdv":
+        rec, avg_us = run_dkdv(args.steps, args.lib)
+        b = budget_dkdv(rec, avg_us)
+    else:
+        rec, avg_us = run(args.steps, args.lib)
+        b = budget(rec, avg_us)
     print(json.dumps(b, indent=1))
     if args.json:
         Path(args.json).write_text(json.dumps(b, indent=1))
