@@ -120,11 +120,11 @@ int make_plan(const mfx_sdpa_args* a, Plan& out) {
 const char* kind_name(const Plan& pl) {
   switch (pl.kind) {
     case Kind::kFlashBf16: {
-      static const char* const names[2][4] = {
-          {"flash_bf16_d32", "flash_bf16_d64", "flash_bf16_d96", "flash_bf16_d128"},
-          {"flash_f16_d32", "flash_f16_d64", "flash_f16_d96", "flash_f16_d128"}};
+      static const char* const names[2][5] = {
+          {"flash_bf16_d32", "flash_bf16_d64", "flash_bf16_d96", "flash_bf16_d128", "flash_bf16_d256"},
+          {"flash_f16_d32", "flash_f16_d64", "flash_f16_d96", "flash_f16_d128", "flash_f16_d256"}};
       const int d = pl.p.D;
-      return names[pl.p.dtype == MFX_F16][d == 32 ? 0 : d == 64 ? 1 : d == 96 ? 2 : 3];
+      return names[pl.p.dtype == MFX_F16][d == 32 ? 0 : d == 64 ? 1 : d == 96 ? 2 : d == 128 ? 3 : 4];
     }
     case Kind::kFlashF32: {
       static const char* const names[2][4] = {

@@ -50,11 +50,14 @@ using tiles::lds_s16x4_t;
 using tiles::s16x4;
 using tiles::tile_swz;
 using tiles::wait_dma;
+using tiles::fence;
 template <int D>
 using TileLoader = tiles::TileLoader<D, kBN, kNT / 64>;
 
+// D = 256: one workgroup per CU (four 32 KB tiles; O, Q and S of a wavefront
+// take ~300 registers).
 template <int D, bool CAUSAL, bool MASK, int E>
-__global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
+__global__ __launch_bounds__(kNT, D > 128 ? 1 : 2) void flash_bf16_kernel(SdpaParams p) {
   __shared__ __attribute__((aligned(16))) bf16 k0[kBN * D];
   __shared__ __attribute__((aligned(16))) bf16 v0[kBN * D];
   __shared__ __attribute__((aligned(16))) bf16 k1[kBN * D];
@@ -93,7 +96,11 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   const int qi = q0 + l32;
 
   int kv_end = Tk;
-  if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kBM));
+  // D = 256 compiles only the causal form (the other spills at this width):
+  // key j is visible to query i when j <= i + co, co = 0 for a causal call
+  // and 2^30 (every key) otherwise.
+  const int co = !p.causal ? (1 << 30) : 0;
+  if (CAUSAL) kv_end = min(Tk, min(Tq + co, (mblk + 1) * kBM + co));
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const TileLoader<D> kload(kp, ks2, Tk, wave, lane), vload(vp, vs2, Tk, wave, lane);
   auto issue = [&](int t, bf16* kl, bf16* vl) {
@@ -137,6 +144,9 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
   // causal diagonal) mask per element; interior tiles do no mask work.
   auto compute = [&](const bf16* kl, const bf16* vl, int kb, auto edge_tag) {
     constexpr bool EDGE = decltype(edge_tag)::value;
+    // D = 256: the phases of a tile (S, softmax, PV) and the tiles stay
+    // apart, so no tile's fragments are live across another's.
+    if constexpr (D > 128) fence();
     f32x16 s[kMT];
     // The two waves of a SIMD alternate between MFMA blocks and softmax
     // work; raising a wave's priority for its MFMA blocks lets the arbiter
@@ -150,9 +160,14 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
       for (int kk = 0; kk < D / 16; ++kk) {
         const bf16x8 a = *reinterpret_cast<const bf16x8*>(&kl[mt * 32 * D + k_off + ((kk * 2 + half) ^ k_sw) * 8]);
         s[mt] = mfma16<E>(a, qf[kk], s[mt]);
+        // D = 256: at most four operand reads run ahead of their MFMAs (all
+        // of a tile's at once do not fit the registers).
+        if constexpr (D > 128)
+          if ((kk & 3) == 3) fence();
       }
     }
     __builtin_amdgcn_s_setprio(0);
+    if constexpr (D > 128) fence();
     // MASK: scores move to the log2 domain here (scale and mask folded);
     // otherwise they stay raw and the scale is folded into the exp2 FMA.
     float mx = -INFINITY;
@@ -169,7 +184,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
                                     b * p.ms[0] + h * p.ms[1] + qi * p.ms[2] + key * p.ms[3]));
         }
         if constexpr (EDGE) {
-          if (key >= Tk || (CAUSAL && key > qi)) x = -INFINITY;
+          if (key >= Tk || (CAUSAL && key > qi + co)) x = -INFINITY;
         }
         s[mt][i] = x;
         mx = fmaxf(mx, x);
@@ -230,6 +245,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
       for (int j = 0; j < kKS; ++j) pb[j] = __builtin_bit_cast(bf16x8, pw[j]);
     }
     l_run += l0 + l1;
+    if constexpr (D > 128) fence();
     __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
@@ -243,13 +259,16 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_kernel(SdpaParams p) {
             (lds_s16x4_t*)(v_rows + 8 * D + ((dt * 4 + v_chunk) ^ v_sw8) * 8));
         const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         o[dt] = mfma16<E>(a, pb[ks], o[dt]);
+        if constexpr (D > 128)
+          if ((ks & 1) == 1) fence();
       }
+    if constexpr (D > 128) fence();
   };
 
   auto step = [&](int t, const bf16* kl, const bf16* vl) {
     const int kb = t * kBN;
-    if (q0 >= Tq || (CAUSAL && kb > q0 + 31)) return;  // nothing of this tile is visible
-    const bool edge = (kb + kBN > Tk) || (CAUSAL && kb + kBN - 1 > q0);
+    if (q0 >= Tq || (CAUSAL && kb > q0 + 31 + co)) return;  // nothing of this tile is visible
+    const bool edge = (kb + kBN > Tk) || (CAUSAL && kb + kBN - 1 > q0 + co);
     if (edge)
       compute(kl, vl, kb, std::true_type{});
     else
@@ -305,7 +324,15 @@ int launch_t(const SdpaParams& p, hipStream_t s) {
 
 template <int D, int E>
 int launch_d(const SdpaParams& p, hipStream_t s) {
-  return p.causal ? launch_t<D, true, true, E>(p, s) : launch_t<D, false, true, E>(p, s);
+  return launch_t<D, true, true, E>(p, s);
+}
+
+// Head size 256, every mask form (the pipelined kernel stops at 128): the
+// causal instantiations serve non-causal calls too (through the kernel's
+// causal offset).
+template <int E>
+int launch_256(const SdpaParams& p, hipStream_t s) {
+  return p.mask ? launch_t<256, true, true, E>(p, s) : launch_t<256, true, false, E>(p, s);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -322,10 +349,10 @@ bool flash_bf16_supports(const SdpaParams& p) {
   // inside it and the last row's tail outside).
   if (p.ks[2] < p.D || p.vs[2] < p.Dv) return false;
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
-  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128)) return false;
+  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128 && p.D != 256)) return false;
   // Masks that vary along query rows run on this file's kernel: head sizes
-  // 64 and 128 only.
-  if (p.mask && p.ms[2] != 0 && p.Tq > 1 && p.D != 64 && p.D != 128) return false;
+  // 64, 128 and 256 only.
+  if (p.mask && p.ms[2] != 0 && p.Tq > 1 && p.D != 64 && p.D != 128 && p.D != 256) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.os[i] % 4) return false;
@@ -336,8 +363,10 @@ bool flash_bf16_supports(const SdpaParams& p) {
 int launch_flash_bf16(const SdpaParams& p, hipStream_t s) {
   // Without an additive mask, or with one that does not vary along query
   // rows, the software-pipelined kernel runs (sdpa_flash_bf16_pipe.hip);
-  // this file's kernel serves masks with a query-row stride.  (With one
-  // query row the pipelined kernel's mask row is that row.)
+  // this file's kernel serves masks with a query-row stride, and head size
+  // 256 in every form.  (With one query row the pipelined kernel's mask row
+  // is that row.)
+  if (p.D == 256) return p.dtype == MFX_F16 ? launch_256<1>(p, s) : launch_256<0>(p, s);
   if (!p.mask || p.ms[2] == 0 || p.Tq == 1) return launch_flash_bf16_pipe(p, s);
   if (p.dtype == MFX_F16) return p.D == 128 ? launch_d<128, 1>(p, s) : launch_d<64, 1>(p, s);
   return p.D == 128 ? launch_d<128, 0>(p, s) : launch_d<64, 0>(p, s);

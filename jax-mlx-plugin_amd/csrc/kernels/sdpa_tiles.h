@@ -26,14 +26,16 @@ constexpr float kSlack = 8.0f;
 // banks whether the LDS serves 128 or 256 bytes per clock: for d = 128 the
 // map is a bijection on each aligned run of 16 rows that is also one-to-one
 // on bits 0-2 for 8 rows and on bits 1-2 and 2-3 for 4 rows; d = 64 rows
-// have only 8 chunks and use a period-8 map.
+// have only 8 chunks and use a period-8 map.  d = 256 rows (512 bytes, two
+// passes over the banks) take the d = 128 map: it stays within each
+// 16-chunk half, so each half is spread as a d = 128 row is.
 template <int D>
 __host__ __device__ constexpr int tile_swz(int r) {
-  if constexpr (D == 128) return (r & 3) | (((r ^ (r >> 2)) & 3) << 2);
+  if constexpr (D >= 128) return (r & 3) | (((r ^ (r >> 2)) & 3) << 2);
   return ((r & 3) << 1) | ((r >> 2) & 1);
 }
 template <int D>
-constexpr int kSwzPeriod = D == 128 ? 16 : 8;
+constexpr int kSwzPeriod = D >= 128 ? 16 : 8;
 
 // LDS operand reads as inline asm at an immediate byte offset from a
 // per-lane LDS address, so the compiler neither batches them nor adds waits

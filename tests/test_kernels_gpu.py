@@ -997,3 +997,58 @@ def test_sdpa_f32_head_sizes_32_96(cuda, nat, oracle, D, tq, tk, hq, hkv, causal
     assert nat.sdpa_kernel_name(q, k, v, causal=causal, mask=maskd).endswith(f"_d{D}")
     out = nat.sdpa(q, k, v, scale=D ** -0.5, causal=causal, mask=maskd)
     check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), D ** -0.5, causal=causal, mask=mask), "f32")
+
+
+# ------------------------------------------------------------ head size 256
+# bf16 / f16 at head size 256 run on the per-element-mask flash kernel (one
+# workgroup per CU: four 32 KB tiles; the pipelined and MFMA decode kernels
+# stop at 128) for every mask form, decode (Tq <= 4) included.  Against the
+# fp64 oracle at the bf16 / f16 bars.
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("tq,tk,hq,hkv,causal", [(100, 77, 3, 3, False), (100, 77, 4, 2, True),
+                                                 (77, 200, 2, 1, True), (129, 129, 3, 3, True),
+                                                 (300, 300, 2, 2, False), (1, 300, 8, 2, False),
+                                                 (4, 1000, 4, 4, True)])
+def test_sdpa_flash_head_size_256(cuda, nat, oracle, dtype, tq, tk, hq, hkv, causal):
+    td = cuda.bfloat16 if dtype == "bf16" else cuda.float16
+    q, k, v = make_qkv(cuda, 81, (2, hq, tq, 256), (2, hkv, tk, 256), td)
+    assert nat.sdpa_kernel_name(q, k, v, causal=causal) == f"flash_{dtype}_d256"
+    out = nat.sdpa(q, k, v, scale=256 ** -0.5, causal=causal)
+    ref = oracle.sdpa(host(q), host(k), host(v), 256 ** -0.5, causal=causal)
+    r = rel_inf(host(out), ref)
+    assert r <= (BF16_REL_TOL if dtype == "bf16" else 5e-3), r
+
+
+@pytest.mark.parametrize("row_mask", [False, True])
+def test_sdpa_flash_head_size_256_masks_layout_qnorm(cuda, nat, oracle, row_mask):
+    """Packed BTNH rows (K and V sliced from one buffer), a padding mask or a
+    per-row bias with -inf holes, and decode with a fused q RMSNorm."""
+    rng = np.random.default_rng(82)
+    B, T, Hq, Hkv, D = 2, 150, 4, 2, 256
+    q = dev(cuda, rng.standard_normal((B, T, Hq, D)), cuda.bfloat16)
+    kv = dev(cuda, rng.standard_normal((B, T, 2 * Hkv, D)), cuda.bfloat16)
+    k, v = kv[:, :, :Hkv], kv[:, :, Hkv:]
+    if row_mask:
+        mask = rng.standard_normal((B, 1, T, T)) * 0.5
+        mask[..., ::7] = -np.inf
+        mask[..., 0] = 0.0
+    else:
+        lens = np.array([150, 61])
+        mask = np.where(np.arange(T)[None] < lens[:, None], 0.0, -np.inf).reshape(B, 1, 1, T)
+    maskd = dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, mask=maskd, layout="bthd") == "flash_bf16_d256"
+    out = nat.sdpa(q, k, v, scale=0.05, mask=maskd, layout="bthd", causal=True)
+    qh, kh, vh = (host(t).transpose(0, 2, 1, 3) for t in (q, k, v))
+    ref = oracle.sdpa(qh, kh, vh, 0.05, mask=mask, causal=True).transpose(0, 2, 1, 3)
+    check_sdpa(out, ref, "bf16")
+    # decode: one query row per head, fused q RMSNorm with a weight
+    qd = dev(cuda, rng.standard_normal((B, Hq, 1, D)), cuda.bfloat16)
+    kd = dev(cuda, rng.standard_normal((B, Hkv, 700, D)), cuda.bfloat16)
+    vd = dev(cuda, rng.standard_normal((B, Hkv, 700, D)), cuda.bfloat16)
+    w = dev(cuda, 1 + 0.1 * rng.standard_normal(D), cuda.bfloat16)
+    assert nat.sdpa_kernel_name(qd, kd, vd) == "flash_bf16_d256"
+    outd = nat.sdpa(qd, kd, vd, scale=0.05, q_rms_eps=1e-6, q_rms_weight=w)
+    qn = oracle.rms_norm(host(qd), host(w), 1e-6)
+    qn = host(cuda.from_numpy(qn.astype(np.float32)).to(cuda.bfloat16))
+    check_sdpa(outd, oracle.sdpa(qn, host(kd), host(vd), 0.05), "bf16")
