@@ -127,11 +127,11 @@ const char* kind_name(const Plan& pl) {
       return names[pl.p.dtype == MFX_F16][d == 32 ? 0 : d == 64 ? 1 : d == 96 ? 2 : d == 128 ? 3 : 4];
     }
     case Kind::kFlashF32: {
-      static const char* const names[2][4] = {
-          {"flash_f32_d32", "flash_f32_d64", "flash_f32_d96", "flash_f32_d128"},
-          {"flash_f32_split_d32", "flash_f32_split_d64", "flash_f32_split_d96", "flash_f32_split_d128"}};
+      static const char* const names[2][5] = {
+          {"flash_f32_d32", "flash_f32_d64", "flash_f32_d96", "flash_f32_d128", "flash_f32_d256"},
+          {"flash_f32_split_d32", "flash_f32_split_d64", "flash_f32_split_d96", "flash_f32_split_d128", ""}};
       const int d = pl.p.D;
-      return names[flash_f32_use_split(pl.p)][d == 32 ? 0 : d == 64 ? 1 : d == 96 ? 2 : 3];
+      return names[flash_f32_use_split(pl.p)][d == 32 ? 0 : d == 64 ? 1 : d == 96 ? 2 : d == 128 ? 3 : 4];
     }
     case Kind::kDecode: return "decode_splitkv";
     case Kind::kDecodeMfma: return "decode_splitkv_mfma";

@@ -31,6 +31,7 @@ constexpr int kNT = 256;
 // 32-bit byte range.
 bool flash_f32_use_split(const SdpaParams& p) {
   const int64_t wgs = (int64_t)((p.Tq + 127) / 128) * p.B * p.Hq;
+  if (p.D > 128) return false;  // head size 256: the row-block kernel only
   for (int64_t st : {p.qs[2], p.ks[2], p.vs[2]})
     if (st < p.D || st >= (int64_t(1) << 24)) return false;
   return wgs < 2LL * device_cu_count() && p.Tk <= 32 * 4 * 8;
@@ -67,9 +68,10 @@ struct Cfg {
 };
 
 // Two workgroups per CU (256 VGPRs) except masked D = 96 and 128, whose
-// extra mask state would spill at that bound.
+// extra mask state would spill at that bound, and D = 256 (Q and O alone
+// take 256 registers; 134 KB of LDS).
 template <int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kNT, (D >= 96 && MASK) ? 1 : 2) void flash_f32_kernel(SdpaParams p) {
+__global__ __launch_bounds__(kNT, (D >= 256 || (D >= 96 && MASK)) ? 1 : 2) void flash_f32_kernel(SdpaParams p) {
   using C = Cfg<D, MASK>;
   __shared__ __attribute__((aligned(16))) float k_lds[2][C::KS * C::KROW];
   __shared__ __attribute__((aligned(16))) float v_lds[2][C::KS * C::VROW];
@@ -525,7 +527,8 @@ int launch_split(const SdpaParams& p, hipStream_t s) {
 
 template <int D, bool CAUSAL, bool MASK>
 int launch_t(const SdpaParams& p, hipStream_t s) {
-  if (flash_f32_use_split(p)) return launch_split<D, CAUSAL, MASK>(p, s);
+  if constexpr (D <= 128)
+    if (flash_f32_use_split(p)) return launch_split<D, CAUSAL, MASK>(p, s);
   const int nmb = (p.Tq + kBM - 1) / kBM;
   const int64_t blocks = (int64_t)nmb * p.B * p.Hq;
   hipLaunchKernelGGL((flash_f32_kernel<D, CAUSAL, MASK>), dim3((unsigned)blocks), dim3(kNT), 0, s,
@@ -546,7 +549,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 bool flash_f32_supports(const SdpaParams& p) {
   if (p.dtype != MFX_F32) return false;
-  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128)) return false;
+  if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128 && p.D != 256)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
     if (p.qs[i] % 4 || p.ks[i] % 4 || p.vs[i] % 4 || p.os[i] % 4) return false;
@@ -562,6 +565,7 @@ int launch_flash_f32(const SdpaParams& p, hipStream_t s) {
     case 32: return launch_d<32>(p, s);
     case 96: return launch_d<96>(p, s);
     case 128: return launch_d<128>(p, s);
+    case 256: return launch_d<256>(p, s);
     default: return launch_d<64>(p, s);
   }
 }

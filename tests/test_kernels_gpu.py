@@ -1052,3 +1052,23 @@ def test_sdpa_flash_head_size_256_masks_layout_qnorm(cuda, nat, oracle, row_mask
     qn = oracle.rms_norm(host(qd), host(w), 1e-6)
     qn = host(cuda.from_numpy(qn.astype(np.float32)).to(cuda.bfloat16))
     check_sdpa(outd, oracle.sdpa(qn, host(kd), host(vd), 0.05), "bf16")
+
+
+@pytest.mark.parametrize("tq,tk,hq,hkv,causal,masked", [(128, 128, 4, 4, False, False), (100, 77, 4, 2, True, False),
+                                                        (33, 300, 4, 1, False, True), (77, 200, 2, 2, True, True),
+                                                        (300, 300, 2, 2, True, False), (1, 500, 4, 2, False, False)])
+def test_sdpa_f32_head_size_256(cuda, nat, oracle, tq, tk, hq, hkv, causal, masked):
+    """The f32 row-block flash kernel at head size 256 (one workgroup per CU,
+    134 KB of LDS; never the key-split kernel): ragged, GQA, causal, an
+    additive mask with -inf holes, a single query row."""
+    q, k, v = make_qkv(cuda, 83, (2, hq, tq, 256), (2, hkv, tk, 256), cuda.float32)
+    mask = None
+    if masked:
+        m = np.random.default_rng(84).standard_normal((2, 1, tq, tk)) * 0.5
+        m[..., ::5] = -np.inf
+        m[..., 0] = 0.0
+        mask = m
+    maskd = None if mask is None else dev(cuda, mask, cuda.float32)
+    assert nat.sdpa_kernel_name(q, k, v, causal=causal, mask=maskd) == "flash_f32_d256"
+    out = nat.sdpa(q, k, v, scale=256 ** -0.5, causal=causal, mask=maskd)
+    check_sdpa(out, oracle.sdpa(host(q), host(k), host(v), 256 ** -0.5, causal=causal, mask=mask), "f32")
