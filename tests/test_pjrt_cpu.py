@@ -394,6 +394,16 @@ def test_sdpa_finite_mask_value_falls_back(api):
     assert steps(d).count("gemm") == 2
 
 
+@pytest.mark.parametrize("D,dt", [(32, "bf16"), (96, "f16"), (256, "bf16"), (256, "f32"), (80, "bf16")])
+def test_sdpa_fuses_at_any_head_size(api, D, dt):
+    """The attention match does not depend on the head size: the module is
+    one fused step at 32, 96, 256 and at 80 (which the kernel library runs on
+    its per-row kernel)."""
+    d = api.inspect(M.sdpa_bhtd_module(B=1, H=2, T=64, D=D, dt=dt, causal=True))
+    assert [n["op"] for n in fused(d)] == ["mfx.sdpa"]
+    assert steps(d) == ["sdpa"]
+
+
 def test_sdpa_transposed_k(api):
     d = api.inspect(M.sdpa_bhtd_module(transposed_k=True, inline_softmax=True))
     assert [n["op"] for n in fused(d)] == ["mfx.sdpa"]

@@ -181,6 +181,22 @@ def test_sdpa_causal_bhtd_bf16(client, oracle):
     assert rel_inf(o, oracle.sdpa(q, k, v, 1 / math.sqrt(128), causal=True)) <= BF16_REL_TOL
 
 
+@pytest.mark.parametrize("D,dt", [(32, "bf16"), (96, "bf16"), (256, "bf16"), (96, "f32"), (256, "f32")])
+def test_sdpa_head_sizes_through_pjrt(client, oracle, D, dt):
+    """The BHTD attention module at head sizes 32, 96 and 256 (bf16) and 96,
+    256 (f32), causal, through Client_Compile / Execute: the rewriter fuses
+    any head size and the kernel library picks the MFMA kernel for it."""
+    rng = np.random.default_rng(95 + D)
+    rnd = bf16_round if dt == "bf16" else (lambda a: a.astype(np.float32))
+    q, k, v = (rnd(rng.standard_normal((1, 4, 200, D))) for _ in range(3))
+    (o,) = run(client, M.sdpa_bhtd_module(B=1, H=4, T=200, D=D, dt=dt, causal=True), [q, k, v], [dt] * 3)
+    ref = oracle.sdpa(q, k, v, 1 / math.sqrt(D), causal=True)
+    if dt == "bf16":
+        assert rel_inf(o, ref) <= BF16_REL_TOL
+    else:
+        assert np.abs(o - ref).max() <= F32_SDPA_TOL
+
+
 def _device_bf16(cuda, a):
     return cuda.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda().bfloat16()
 
