@@ -308,7 +308,7 @@ def build_kernels() -> Path:
     return out
 
 
-PHASE_TIMER_FILES = {"sdpa_flash_bf16_pipe.hip", "sdpa_bwd_mfma.hip"}
+PHASE_TIMER_FILES = {"sdpa_flash_bf16_pipe.hip", "sdpa_bwd_mfma.hip", "sdpa_decode_mfma.hip"}
 
 
 def build_phase_timers() -> Path:

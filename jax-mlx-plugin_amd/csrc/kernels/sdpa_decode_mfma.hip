@@ -41,6 +41,12 @@
 #include "sdpa_elem.h"
 #include "sdpa_tiles.h"
 
+#if defined(MFX_PHASE_TIMERS)
+#define PHASE(...) __VA_ARGS__
+#else
+#define PHASE(...)
+#endif
+
 namespace mfx {
 namespace {
 
@@ -48,6 +54,7 @@ using tiles::kSlack;
 using tiles::lds_void_t;
 using tiles::s16x4;
 using tiles::tile_swz;
+using tiles::fence;
 
 constexpr int kDN = 32;  // keys per tile: three stages = 48 KB of LDS per workgroup at d = 128
 constexpr int kMT = kDN / 32;
@@ -216,6 +223,22 @@ __device__ __forceinline__ int64_t range_start(int w, int64_t T, int W) { return
 // D: features per row of the LDS tiles (64 or 128); DV <= D: the head size
 // (a multiple of 32).  Rows load D wide and only features below DV reach an
 // MFMA, as in the pipelined prefill kernel.
+#if defined(MFX_PHASE_TIMERS)
+// Diagnostic build: one record of kDecPhaseFields u64 per decode wavefront
+// (blockIdx.x): 0 ids (XCC id, HW_ID, wavefront), 1-5 realtime stamps (low
+// words, 100 MHz) at its start, when its range is found, when the first
+// segment's first tiles are issued, at its first tile, at the end of its last
+// segment's tiles, 6 realtime end (64 bits), 7 tiles, 8 segments, 9 total
+// cycles, 10 cycles in the tile loops.  The kernel's SGPRs are all taken, so
+// the values wait in per-lane LDS words until the end; every stamp is taken
+// where none of the kernel's inline-asm LDS reads is outstanding.
+constexpr int kDecPhaseRecords = 1 << 15;
+constexpr int kDecPhaseFields = 12;
+__device__ unsigned long long g_dec_phase_records[kDecPhaseRecords * kDecPhaseFields];
+enum DecPhaseSlot { kDpStart, kDpRange, kDpIssue, kDpFirst, kDpStreamEnd, kDpTiles, kDpSegs, kDpCStart, kDpCStream,
+                    kDpCLoop, kDecPhaseSlots };
+#endif
+
 template <int D, int DV, int MT, bool MB, bool CAUSAL, int E>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   static_assert(DV % 32 == 0 && DV <= D && D - DV < 64, "head size");
@@ -235,6 +258,15 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
   const int lane = threadIdx.x;
   const int half = lane >> 5, col = lane & 31;
   const int w = blockIdx.x, W = gridDim.x;
+#if defined(MFX_PHASE_TIMERS)
+  __shared__ unsigned dph[kDecPhaseSlots * 64];
+  auto dslot = [&](int f) -> unsigned& { return dph[f * 64 + lane]; };
+  auto dnow = []() { return (unsigned)__builtin_amdgcn_s_memtime(); };
+  auto dreal = []() { return (unsigned)__builtin_amdgcn_s_memrealtime(); };
+  for (int f = 0; f < kDecPhaseSlots; ++f) dslot(f) = 0;
+  dslot(kDpStart) = dreal();
+  dslot(kDpCStart) = dnow();
+#endif
   const int BHk = p.B * p.Hkv;
   const int Tq = p.Tq, R = p.group * Tq, Tk = p.Tk;
   const float sl2 = p.scale_log2;  // > 0 (checked on the host)
@@ -296,6 +328,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     }
     P += __builtin_amdgcn_readlane(incl, 63);
   }
+  PHASE(fence(); dslot(kDpRange) = dreal(); fence();)
 
   // Per-lane byte offsets of the operand reads within a tile (the same
   // patterns as the prefill kernel).
@@ -573,6 +606,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     // program order.
     issue(tile_at(0), k0, v0);
     if (ntl > 1) issue(tile_at(1), k1, v1);
+    PHASE(fence(); if (dslot(kDpSegs) == 0) dslot(kDpIssue) = dreal(); fence();)
     // Rows past R are zero (never stored); optional RMSNorm in fp32, rounded
     // to bf16 as the unfused graph rounds its output.
 #pragma unroll
@@ -620,6 +654,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
         qf[kk] = f32_frag_f16(x);
       }
     }
+    PHASE(fence(); if (dslot(kDpSegs) == 0) dslot(kDpFirst) = dreal(); dslot(kDpCLoop) = dnow(); fence();)
     for (int i = 0; i < ntl; i += 3) {
       body(i, k0, v0, k2, v2);
       if (i + 1 >= ntl) break;
@@ -627,6 +662,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
       if (i + 2 >= ntl) break;
       body(i + 2, k2, v2, k1, v1);
     }
+    PHASE(fence(); dslot(kDpStreamEnd) = dreal(); dslot(kDpCStream) += dnow() - dslot(kDpCLoop);
+          dslot(kDpTiles) += (unsigned)ntl; dslot(kDpSegs) += 1u; fence();)
 
     // Lanes col and col+32 hold the two halves of each row's keys.
     float lt;
@@ -652,6 +689,30 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
     ++bhk;
     while (s < e && bhk < BHk && count_of(bhk) == 0) ++bhk;
   }
+#if defined(MFX_PHASE_TIMERS)
+  {
+    fence();
+    unsigned xcc, hwid;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+    const unsigned c_end = dnow();
+    const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && w < kDecPhaseRecords) {
+      unsigned long long* r = g_dec_phase_records + (size_t)w * kDecPhaseFields;
+      r[0] = (unsigned long long)(xcc & 0xff) | ((unsigned long long)hwid << 8) | ((unsigned long long)w << 40);
+      r[1] = dslot(kDpStart);
+      r[2] = dslot(kDpRange);
+      r[3] = dslot(kDpIssue);
+      r[4] = dslot(kDpFirst);
+      r[5] = dslot(kDpStreamEnd);
+      r[6] = rt_end;
+      r[7] = dslot(kDpTiles);
+      r[8] = dslot(kDpSegs);
+      r[9] = c_end - dslot(kDpCStart);
+      r[10] = dslot(kDpCStream);
+    }
+  }
+#endif
 }
 
 // Merges the partial (m, l, O) rows of each output row: one wavefront per
@@ -924,3 +985,25 @@ int launch_decode_mfma(const SdpaParams& p, hipStream_t s) {
 #endif
 
 }  // namespace mfx
+
+#if defined(MFX_PHASE_TIMERS) && !defined(MFX_DECODE_WIDE)
+// Diagnostic build only: copies up to max_records decode phase records
+// (kDecPhaseFields u64 each, fields as written at the end of
+// decode_mfma_kernel) to host memory after the device is idle and returns how
+// many the device array holds; clear != 0 zeroes the array afterwards.  Not
+// part of the product's C ABI.
+extern "C" __attribute__((visibility("default"))) int64_t mfx_decode_phase_timers_read(void* host,
+                                                                                       int64_t max_records,
+                                                                                       int clear) {
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  void* dev = nullptr;
+  if (hipGetSymbolAddress(&dev, HIP_SYMBOL(mfx::g_dec_phase_records)) != hipSuccess) return -1;
+  const int64_t n = max_records < mfx::kDecPhaseRecords ? max_records : mfx::kDecPhaseRecords;
+  if (host && n > 0 &&
+      hipMemcpy(host, dev, (size_t)n * mfx::kDecPhaseFields * 8, hipMemcpyDeviceToHost) != hipSuccess)
+    return -1;
+  if (clear && hipMemset(dev, 0, sizeof(mfx::g_dec_phase_records)) != hipSuccess) return -1;
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  return mfx::kDecPhaseRecords;
+}
+#endif

@@ -4,6 +4,7 @@ per-block budget of the SDPA backward's dK/dV kernel on the same shape.
     python jax-mlx-plugin_amd/build.py phase_timers
     python jax-mlx-plugin_amd/phase_budget.py [--json out.json]
     python jax-mlx-plugin_amd/phase_budget.py --kernel dkdv [--json out.json]
+    python jax-mlx-plugin_amd/phase_budget.py --kernel decode [--json out.json]
 
 Loads the diagnostic copy of libmfx_kernels.so built with -DMFX_PHASE_TIMERS
 (jax_mlx_amd/lib/phase_timers/), runs causal bf16 SDPA on config 3's inputs
@@ -28,6 +29,13 @@ with this block's exp2 / dS work) and its barrier phase (per 64-query tile:
 vmcnt wait, s_barrier, the next tile's DMA issue), against the MFMA floor
 (one wavefront per SIMD, 32 MFMAs per block).
 
+With --kernel decode it runs config 5 (GQA decode, q [16,32,1,128] bf16
+with RMSNorm, k / v [16,8,8192,128], a length mask, all from
+numpy.random.default_rng(5) in bench.py's order) and reads the records of
+decode_mfma_kernel (sdpa_decode_mfma.hip): per wavefront, the time to find
+its range of the tile lists, to issue its first tiles, until its first tile
+and while it streams its tiles, and the spread between XCDs.
+
 The instrumented kernels run a few percent slower than the shipped ones (a
 handful of s_memtime reads per tile); shares of the budget are what it is for.
 """
@@ -50,6 +58,8 @@ WAVES_PER_SIMD = 2
 FIELDS = 20             # u64 per wavefront record (PhaseClock, kPhaseFields)
 BWD_FIELDS = 16         # u64 per dK/dV wavefront record (kBwdPhaseFields)
 BWD_MFMAS_PER_BLOCK = 32  # S, dP, dV, dK: 8 each per 32-query block at d = 128
+DEC_FIELDS = 12         # u64 per decode wavefront record (kDecPhaseFields)
+DEC_TILE_BYTES = 2 * 32 * 128 * 2  # K and V of one 32-key tile at d = 128, bf16
 
 
 def run(steps: int, lib_path: Path = LIB):
@@ -205,6 +215,102 @@ def budget_dkdv(rec: np.ndarray, avg_us: float) -> dict:
     }
 
 
+def run_decode(steps: int, lib_path: Path = LIB):
+    import ctypes
+
+    import torch
+
+    sys.path.insert(0, str(PKG))
+    from jax_mlx_amd import native
+
+    lib = native.load(lib_path, make_default=True)
+    lib.mfx_decode_phase_timers_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    lib.mfx_decode_phase_timers_read.restype = ctypes.c_int64
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, d, S = 16, 32, 8, 128, 8192
+    draw = lambda shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda().bfloat16()  # noqa
+    q = draw((B, Hq, 1, d))
+    kvs = [(draw((B, Hkv, S, d)), draw((B, Hkv, S, d)))]
+    lens = rng.integers(1024, 8192, size=B, endpoint=True)
+    # a second K / V set, alternated as bench.py does, so no call finds its
+    # K / V in the 256 MB Infinity Cache
+    kvs.append((draw((B, Hkv, S, d)), draw((B, Hkv, S, d))))
+    mask = torch.from_numpy(np.where(np.arange(S)[None] < lens[:, None], 0.0, -np.inf)
+                            .reshape(B, 1, 1, S).astype(np.float32)).cuda()
+    out = torch.empty_like(q)
+    it = [0]
+
+    def call():
+        k, v = kvs[it[0] % 2]
+        it[0] += 1
+        native.sdpa(q, k, v, scale=d ** -0.5, mask=mask, q_rms_eps=1e-6, out=out)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.25:
+        for _ in range(10):
+            call()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    avg_us = e0.elapsed_time(e1) * 1e3 / steps
+    cap = lib.mfx_decode_phase_timers_read(None, 0, 1)   # clear
+    call()
+    n = 4096
+    rec = np.zeros((n, DEC_FIELDS), dtype=np.uint64)
+    got = lib.mfx_decode_phase_timers_read(rec.ctypes.data, n, 0)
+    if got < 0 or cap < n:
+        raise RuntimeError("reading the phase records failed")
+    return rec, avg_us, int(lens.sum())
+
+
+def budget_decode(rec: np.ndarray, avg_us: float, sum_len: int) -> dict:
+    rec = rec[rec[:, 6] != 0]
+    if not len(rec):
+        raise RuntimeError("no phase records written: the kernel that ran was not the phase-timer build")
+    ids, rt_end = rec[:, 0], rec[:, 6].astype(np.int64)
+    back = lambda f: rt_end - ((rec[:, 6] & 0xffffffff).astype(np.int64) - rec[:, f].astype(np.int64)) % (1 << 32)  # noqa
+    rt = {name: back(f) for name, f in (("start", 1), ("range", 2), ("issue", 3), ("first", 4), ("stream_end", 5))}
+    tiles = rec[:, 7].astype(np.float64)
+    t0 = rt["start"].min()
+    span_us = (rt_end.max() - t0) / RT_HZ * 1e6
+    us = lambda a: float(np.median(a) / RT_HZ * 1e6)  # noqa: E731
+    stream_us = (rt["stream_end"] - rt["first"]) / RT_HZ * 1e6
+    xcc = (ids & 0xff).astype(np.int64)
+    xcd_stream = {int(x): round(float(np.median(stream_us[xcc == x])), 2) for x in np.unique(xcc)}
+    xcd_end = {int(x): round(float((rt_end[xcc == x].max() - t0) / RT_HZ * 1e6), 2) for x in np.unique(xcc)}
+    # aggregate rate while streaming: every tile's K / V bytes over the span
+    # from the median first tile to the median stream end (the run alternates
+    # two K / V sets, so these bytes come from HBM)
+    stream_span_s = float(np.median(rt["stream_end"]) - np.median(rt["first"])) / RT_HZ
+    clock_mhz = float(np.median(rec[:, 9].astype(np.float64) / ((rt_end - rt["start"]) / RT_HZ)) / 1e6)
+    return {
+        "kernel": "decode_mfma_kernel<128, f32 mask, shared rows>",
+        "call_avg_us_instrumented": round(avg_us, 2),
+        "main_kernel_span_us": round(span_us, 2),
+        "shader_clock_mhz": round(clock_mhz, 1),
+        "wavefronts": int(len(rec)), "tiles": int(tiles.sum()), "mean_tiles_per_wavefront": round(float(tiles.mean()), 2),
+        "valid_kv_bytes": 2 * 8 * 128 * 2 * sum_len,
+        "median_us": {
+            "start_to_range": round(us(rt["range"] - rt["start"]), 3),
+            "range_to_first_issue": round(us(rt["issue"] - rt["range"]), 3),
+            "first_issue_to_first_tile": round(us(rt["first"] - rt["issue"]), 3),
+            "streaming": round(float(np.median(stream_us)), 3),
+            "stream_end_to_end": round(us(rt_end - rt["stream_end"]), 3),
+            "start_to_end": round(us(rt_end - rt["start"]), 3),
+            "last_end_after_first_start": round(span_us, 3)},
+        "p10_p90_streaming_us": [round(float(np.percentile(stream_us, 10)), 2),
+                                 round(float(np.percentile(stream_us, 90)), 2)],
+        "tb_per_s_while_streaming": round(tiles.sum() * DEC_TILE_BYTES / stream_span_s / 1e12, 2),
+        "xcd_median_streaming_us": xcd_stream,
+        "xcd_finish_us": xcd_end,
+        "xcd_finish_spread_us": round(max(xcd_end.values()) - min(xcd_end.values()), 2),
+        "segments_per_wavefront_max": int(rec[:, 8].max()),
+    }
+
+
 def budget(rec: np.ndarray, avg_us: float) -> dict:
     rec = rec[rec[:, 4] != 0]
     if not len(rec):
@@ -263,8 +369,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--json", help="also write the budget here")
     ap.add_argument("--lib", type=Path, default=LIB, help="a phase-timer build of libmfx_kernels.so")
-    ap.add_argument("--kernel", choices=("flash", "dkdv"), default="flash",
-                    help="flash: the config-3 forward; dkdv: the backward's dK/dV kernel on the same shape")
+    ap.add_argument("--kernel", choices=("flash", "dkdv", "decode"), default="flash",
+                    help="flash: the config-3 forward; dkdv: the backward's dK/dV kernel on the same shape; "
+                         "decode: config 5's MFMA decode")
     args = ap.parse_args()
     if not args.lib.exists():
         print(f"{args.lib} is not built: python jax-mlx-plugin_amd/build.py phase_timers", file=sys.stderr)
@@ -272,6 +379,9 @@ def main() -> int:
     if args.kernel == "dkdv":
         rec, avg_us = run_dkdv(args.steps, args.lib)
         b = budget_dkdv(rec, avg_us)
+    elif args.kernel == "decode":
+        rec, avg_us, sum_len = run_decode(args.steps, args.lib)
+        b = budget_decode(rec, avg_us, sum_len)
     else:
         rec, avg_us = run(args.steps, args.lib)
         b = budget(rec, avg_us)

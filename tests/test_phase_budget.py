@@ -71,3 +71,35 @@ def test_occupancy_counts_waves_per_simd():
 def test_dkdv_budget_rejects_empty_records():
     with pytest.raises(RuntimeError, match="phase-timer build"):
         pb.budget_dkdv(np.zeros((4, pb.BWD_FIELDS), dtype=np.uint64), 1.0)
+
+
+def test_decode_budget_medians_and_rates():
+    """Three wavefronts on two XCDs: per-phase medians from the realtime
+    stamps (low words rebuilt against the 64-bit end), tiles and the
+    streaming rate over the median streaming span."""
+    base = (1 << 32) - 30
+    rows = []
+    # (xcc, start, range, issue, first, stream_end, end, tiles)
+    for xcc, st, rg, iss, fi, se, en, t in ((0, 0, 200, 300, 450, 4450, 4500, 20), (0, 10, 210, 320, 460, 4460, 4520, 20),
+                                            (1, 0, 250, 350, 500, 5000, 5050, 22)):
+        r = np.zeros(pb.DEC_FIELDS, dtype=np.uint64)
+        r[0] = _ids(xcc, 0, 0)
+        for f, v in ((1, st), (2, rg), (3, iss), (4, fi), (5, se)):
+            r[f] = (base + v) & 0xffffffff
+        r[6] = base + en
+        r[7], r[8] = t, 1
+        r[9] = (en - st) * 20                         # 2.0 GHz
+        rows.append(r)
+    b = pb.budget_decode(np.stack(rows), avg_us=70.0, sum_len=1000)
+    m = b["median_us"]
+    tick = 1e6 / RT
+    assert m["start_to_range"] == pytest.approx(200 * tick)
+    assert m["range_to_first_issue"] == pytest.approx(100 * tick)      # 100, 110, 100
+    assert m["first_issue_to_first_tile"] == pytest.approx(150 * tick)  # 150, 140, 150
+    assert m["streaming"] == pytest.approx(4000 * tick)
+    assert b["tiles"] == 62 and b["shader_clock_mhz"] == pytest.approx(2000.0)
+    assert b["main_kernel_span_us"] == pytest.approx(5050 * tick)
+    # 62 tiles x 16 KB over the median first-tile-to-stream-end span
+    span_s = (4460 - 460) / RT
+    assert b["tb_per_s_while_streaming"] == pytest.approx(round(62 * pb.DEC_TILE_BYTES / span_s / 1e12, 2))
+    assert b["xcd_finish_spread_us"] == pytest.approx(round((5050 - 4520) * tick, 2))
