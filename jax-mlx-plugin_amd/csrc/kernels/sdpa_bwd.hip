@@ -17,7 +17,11 @@
 // f16, and every mask; one wavefront owns one output row and walks the other
 // axis in chunks of 64 (one score per lane), then accumulates its row with
 // lanes over features.  They are correct, not fast: bf16 and f16 with head
-// size 64 / 128 run on the matrix-core kernels (sdpa_bwd_mfma.hip).
+// size 64 / 128 run on the matrix-core kernels (sdpa_bwd_mfma.hip), and head
+// sizes 32 / 96 too, on copies of q, k, v, dO and O zero-padded to 64 / 128
+// features in the workspace (the padded features add zero to every score and
+// to delta, and their gradients, zero, are not copied out).
+#include <algorithm>
 #include <cmath>
 
 #include "sdpa_common.h"
@@ -178,11 +182,43 @@ __global__ __launch_bounds__(64) void bwd_dkdv_generic(SdpaBwdParams p) {
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Copies rows [rows][D] (element strides s0..s2 over (b, h, t), feature
+// stride 1) into contiguous rows of Dp >= D features, the rest zero; or back
+// (unpad: the first D features of each contiguous row to the strided rows).
+// One thread per 16-byte chunk (D and Dp multiples of 8 elements).
+template <bool UNPAD>
+__global__ __launch_bounds__(256) void pad_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                       int64_t rows, int D, int Dp, int H, int T, int64_t s0,
+                                                       int64_t s1, int64_t s2) {
+  const int cpr = Dp / 8;  // chunks per padded row
+  const int64_t n = rows * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cpr;
+    const int c = (int)(i % cpr) * 8;
+    const int t = (int)(r % T);
+    const int64_t bh = r / T;
+    const int64_t strided = (bh / H) * s0 + (bh % H) * s1 + t * s2 + c;
+    if constexpr (UNPAD) {
+      if (c < D) *reinterpret_cast<uint4*>(dst + strided) = *reinterpret_cast<const uint4*>(src + r * Dp + c);
+    } else {
+      uint4 v = {0u, 0u, 0u, 0u};
+      if (c < D) v = *reinterpret_cast<const uint4*>(src + strided);
+      *reinterpret_cast<uint4*>(dst + r * Dp + c) = v;
+    }
+  }
+}
+
 struct BwdPlan {
   SdpaBwdParams p{};
   SdpaParams fwd{};
   bool mfma = false;
   size_t o_bytes = 0, row_bytes = 0;  // workspace: O, then lse, then delta
+  // Head size 32 / 96 on the matrix-core kernels: pp is p on rows padded to
+  // dp features (q, k, v, dO, O and dq, dk, dv in the workspace after
+  // delta; pointers bound at launch).
+  int dp = 0;
+  SdpaBwdParams pp{};
+  size_t q_pad = 0, kv_pad = 0;  // bytes of one padded [B,Hq,Tq,dp] / [B,Hkv,Tk,dp] tensor
 };
 
 int make_bwd_plan(const mfx_sdpa_bwd_args* a, BwdPlan& out) {
@@ -290,10 +326,64 @@ int make_bwd_plan(const mfx_sdpa_bwd_args* a, BwdPlan& out) {
   f.num_splits = 1;
   f.split_len = p.Tk;
   out.mfma = bwd_mfma_supports(p);
+  // The copies move 16-byte chunks: every tensor 16-byte aligned with
+  // strides of whole chunks (the recomputed O is the workspace's).
+  auto chunked = [&]() {
+    const void* ptrs[8] = {p.q, p.k, p.v, p.dout, p.dq, p.dk, p.dv, saved ? p.o : nullptr};
+    for (const void* ptr : ptrs)
+      if ((uintptr_t)ptr % 16) return false;
+    for (int i = 0; i < 3; ++i)
+      if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.dos[i] % 8 || p.os[i] % 8 || p.dqs[i] % 8 ||
+          p.dks[i] % 8 || p.dvs[i] % 8)
+        return false;
+    return true;
+  };
+  if (!out.mfma && (p.dtype == MFX_BF16 || p.dtype == MFX_F16) && p.D == p.Dv && (p.D == 32 || p.D == 96) &&
+      chunked()) {
+    // The matrix-core kernels on zero-padded copies: contiguous rows of dp
+    // features (pointers null until launch; the workspace is 256-byte
+    // aligned and every region a multiple of 256 bytes).
+    SdpaBwdParams pp = p;
+    const int dp = p.D == 32 ? 64 : 128;
+    pp.D = pp.Dv = dp;
+    const int64_t qst[4] = {(int64_t)p.Hq * p.Tq * dp, (int64_t)p.Tq * dp, dp, 1};
+    const int64_t kst[4] = {(int64_t)p.Hkv * p.Tk * dp, (int64_t)p.Tk * dp, dp, 1};
+    for (int i = 0; i < 4; ++i) {
+      pp.qs[i] = pp.dos[i] = pp.os[i] = pp.dqs[i] = qst[i];
+      pp.ks[i] = pp.vs[i] = pp.dks[i] = pp.dvs[i] = kst[i];
+    }
+    pp.q = pp.k = pp.v = pp.dout = pp.o = nullptr;
+    pp.dq = pp.dk = pp.dv = nullptr;
+    if (bwd_mfma_supports(pp)) {
+      out.dp = dp;
+      out.pp = pp;
+      out.q_pad = align256((size_t)rows * dp * 2);
+      out.kv_pad = align256((size_t)p.B * p.Hkv * p.Tk * dp * 2);
+    }
+  }
   return MFX_OK;
 }
 
-size_t bwd_workspace(const BwdPlan& pl) { return pl.o_bytes + 2 * pl.row_bytes; }
+// Workspace: O (recomputed), lse, delta; with padding, then Q, dO, O, dQ
+// (q_pad each) and K, V, dK, dV (kv_pad each).
+size_t bwd_workspace(const BwdPlan& pl) {
+  return pl.o_bytes + 2 * pl.row_bytes + (pl.dp ? 4 * pl.q_pad + 4 * pl.kv_pad : 0);
+}
+
+// Pads (or unpads) one [B, H, T, D] tensor with element strides st.
+int pad_rows(const void* src, void* dst, const BwdPlan& pl, int H, int T, const int64_t* st, bool unpad,
+             hipStream_t s) {
+  const int64_t rows = (int64_t)pl.p.B * H * T;
+  const int64_t chunks = rows * (pl.dp / 8);
+  const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 4096);
+  if (unpad)
+    hipLaunchKernelGGL((pad_rows_kernel<true>), dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(src),
+                       static_cast<uint16_t*>(dst), rows, pl.p.D, pl.dp, H, T, st[0], st[1], st[2]);
+  else
+    hipLaunchKernelGGL((pad_rows_kernel<false>), dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(src),
+                       static_cast<uint16_t*>(dst), rows, pl.p.D, pl.dp, H, T, st[0], st[1], st[2]);
+  return launch_status("pad_rows_kernel");
+}
 
 }  // namespace
 }  // namespace mfx
@@ -309,6 +399,10 @@ size_t mfx_sdpa_bwd_workspace_size(const mfx_sdpa_bwd_args* args) {
 const char* mfx_sdpa_bwd_kernel_name(const mfx_sdpa_bwd_args* args) {
   mfx::BwdPlan pl;
   if (mfx::make_bwd_plan(args, pl) != MFX_OK) return nullptr;
+  if (pl.dp) {
+    static const char* const padded[2][2] = {{"mfma_bf16_d32", "mfma_bf16_d96"}, {"mfma_f16_d32", "mfma_f16_d96"}};
+    return padded[pl.p.dtype == MFX_F16][pl.p.D == 96];
+  }
   if (!pl.mfma) return "generic";
   if (pl.p.dtype == MFX_F16) return pl.p.D == 128 ? "mfma_f16_d128" : "mfma_f16_d64";
   return pl.p.D == 128 ? "mfma_bf16_d128" : "mfma_bf16_d64";
@@ -348,6 +442,39 @@ int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream) {
   }
 
   if (pl.mfma) return launch_bwd_mfma(p, s);
+  if (pl.dp) {
+    // Zero-padded copies in, the matrix-core kernels, the gradients out.
+    char* w = ws + pl.o_bytes + 2 * pl.row_bytes;
+    SdpaBwdParams& pp = pl.pp;
+    void* qp = w;
+    void* dop = w + pl.q_pad;
+    void* op = w + 2 * pl.q_pad;
+    void* dqp = w + 3 * pl.q_pad;
+    char* wk = w + 4 * pl.q_pad;
+    void* kp = wk;
+    void* vp = wk + pl.kv_pad;
+    void* dkp = wk + 2 * pl.kv_pad;
+    void* dvp = wk + 3 * pl.kv_pad;
+    if ((rc = pad_rows(p.q, qp, pl, p.Hq, p.Tq, p.qs, false, s)) != MFX_OK) return rc;
+    if ((rc = pad_rows(p.dout, dop, pl, p.Hq, p.Tq, p.dos, false, s)) != MFX_OK) return rc;
+    if ((rc = pad_rows(p.o, op, pl, p.Hq, p.Tq, p.os, false, s)) != MFX_OK) return rc;
+    if ((rc = pad_rows(p.k, kp, pl, p.Hkv, p.Tk, p.ks, false, s)) != MFX_OK) return rc;
+    if ((rc = pad_rows(p.v, vp, pl, p.Hkv, p.Tk, p.vs, false, s)) != MFX_OK) return rc;
+    pp.q = qp;
+    pp.dout = dop;
+    pp.o = op;
+    pp.k = kp;
+    pp.v = vp;
+    pp.dq = dqp;
+    pp.dk = dkp;
+    pp.dv = dvp;
+    pp.lse = p.lse;
+    pp.delta = p.delta;
+    if ((rc = launch_bwd_mfma(pp, s)) != MFX_OK) return rc;
+    if ((rc = pad_rows(dqp, p.dq, pl, p.Hq, p.Tq, p.dqs, true, s)) != MFX_OK) return rc;
+    if ((rc = pad_rows(dkp, p.dk, pl, p.Hkv, p.Tk, p.dks, true, s)) != MFX_OK) return rc;
+    return pad_rows(dvp, p.dv, pl, p.Hkv, p.Tk, p.dvs, true, s);
+  }
   const int64_t rows = (int64_t)p.B * p.Hq * p.Tq;
   const unsigned dblocks = (unsigned)((rows + 3) / 4);
   if (p.dtype == MFX_BF16)

@@ -261,6 +261,16 @@ def test_sdpa_f16_bwd_btnh_gqa_mask(cuda, nat, oracle):
     bwd_case(cuda, nat, oracle, 42, (2, 96, 8, 64), (2, 160, 2, 64), mask=mask, layout="bthd", scale=0.2)
 
 
+@pytest.mark.parametrize("D,tq,tk,causal", [(32, 64, 64, True), (96, 200, 200, True), (96, 77, 130, False),
+                                            (32, 1, 33, False)])
+def test_sdpa_f16_bwd_padded_head_sizes(cuda, nat, oracle, D, tq, tk, causal):
+    """Head sizes 32 / 96 on the matrix-core backward through zero-padded
+    64- / 128-feature copies."""
+    q, k, v = make_qkv(cuda, 33, (1, 2, tq, D), (1, 2, tk, D))
+    assert nat.sdpa_bwd_kernel_name(q, k, v, causal=causal) == f"mfma_f16_d{D}"
+    bwd_case(cuda, nat, oracle, 33, (1, 2, tq, D), (1, 2, tk, D), causal=causal)
+
+
 def test_sdpa_f16_bwd_generic_head_size(cuda, nat, oracle):
     q, k, v = make_qkv(cuda, 43, (1, 3, 50, 80), (1, 3, 70, 80))
     assert nat.sdpa_bwd_kernel_name(q, k, v, causal=True) == "generic"

@@ -761,6 +761,39 @@ def test_sdpa_bwd_btnh_gqa_mask(cuda, nat, oracle, dtype):
     check_grads(grads, refs, dtype)
 
 
+@pytest.mark.parametrize("D", [32, 96])
+@pytest.mark.parametrize("tq,tk,hq,hkv,causal", [(64, 64, 2, 2, True), (200, 200, 4, 2, True), (77, 130, 2, 1, False),
+                                                 (1, 33, 2, 2, False)])
+def test_sdpa_bwd_padded_head_sizes(cuda, nat, oracle, D, tq, tk, hq, hkv, causal):
+    """bf16 head sizes 32 / 96 on the matrix-core backward: q, k, v, dO and O
+    copied into zero-padded 64- / 128-feature rows, the gradients copied out."""
+    q, k, v = make_qkv(cuda, 91, (1, hq, tq, D), (1, hkv, tk, D), cuda.bfloat16)
+    assert nat.sdpa_bwd_kernel_name(q, k, v, causal=causal) == f"mfma_bf16_d{D}"
+    grads, refs = bwd_case(cuda, nat, oracle, 91, (1, hq, tq, D), (1, hkv, tk, D), "bf16", causal=causal)
+    check_grads(grads, refs, "bf16")
+
+
+@pytest.mark.parametrize("D", [32, 96])
+def test_sdpa_bwd_padded_btnh_mask_and_residuals(cuda, nat, oracle, D):
+    """The padded route on BTNH views with GQA and a per-row mask, and from a
+    forward's output and lse: the same gradients as the recomputing call."""
+    rng = np.random.default_rng(92)
+    m = rng.standard_normal((2, 1, 96, 160)).astype(np.float32)
+    m[:, :, :, 5] = -np.inf
+    mask = dev(cuda, m, cuda.float32)
+    grads, refs = bwd_case(cuda, nat, oracle, 93, (2, 96, 8, D), (2, 160, 2, D), "bf16", mask=mask, layout="bthd",
+                           scale=0.2)
+    check_grads(grads, refs, "bf16")
+    q, k, v = make_qkv(cuda, 94, (2, 4, 130, D), (2, 2, 130, D), cuda.bfloat16)
+    g = dev(cuda, rng.standard_normal((2, 4, 130, D)), cuda.bfloat16)
+    lse = cuda.empty(2 * 4 * 130, dtype=cuda.float32, device="cuda")
+    out = nat.sdpa(q, k, v, causal=True, lse=lse)
+    re = nat.sdpa_bwd(q, k, v, g, causal=True)
+    fw = nat.sdpa_bwd(q, k, v, g, causal=True, fwd_out=out, fwd_lse=lse)
+    for a, b in zip(re, fw):
+        assert cuda.equal(a, b)
+
+
 def test_sdpa_bwd_odd_head_size_generic(cuda, nat, oracle):
     grads, refs = bwd_case(cuda, nat, oracle, 43, (1, 3, 50, 80), (1, 3, 70, 80), "bf16", causal=True,
                            vshape=(1, 3, 70, 48))
