@@ -123,7 +123,8 @@ def test_custom_call_layer_norm_bwd(client, oracle, shape, dt, pdt):
 
 
 @pytest.mark.parametrize("dt,B,T,N,K,H,S", [("f32", 2, 64, 4, 4, 64, 64), ("bf16", 1, 128, 8, 2, 128, 160),
-                                             ("bf16", 2, 96, 4, 4, 64, 96)])
+                                             ("bf16", 2, 96, 4, 4, 64, 96), ("bf16", 1, 100, 4, 2, 96, 130),
+                                             ("bf16", 2, 64, 2, 2, 32, 64)])
 def test_custom_call_sdpa_bwd(client, oracle, dt, B, T, N, K, H, S):
     """custom_call @mlx_sdpa_bwd (reference src/jax_mlx_pjrt.cpp:8151-8206):
     BTNH gradients against the fp64 closed form."""
