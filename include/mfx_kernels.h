@@ -164,7 +164,9 @@ size_t mfx_layer_norm_bwd_workspace_size(const mfx_norm_bwd_args* args);
  *
  * dtype is MFX_F32, MFX_BF16 or MFX_F16 (fp32 accumulation for all; the
  * 16-bit paths feed probabilities rounded to `dtype` to the PV product, as
- * JAX's attention casts them to the value dtype).
+ * JAX's attention casts them to the value dtype).  Head sizes D == Dv of 32,
+ * 64, 96, 128 and 256 run on the matrix-core kernels (mfx_sdpa_kernel_name
+ * names the one a call takes); any other up to 256 on a per-row kernel.
  *
  * lse (optional output): the row log-sum-exp of the scaled, masked scores in
  * log2 units, lse[(b * Hq + h) * Tq + i] = log2(sum_j exp2(log2e * (scale *
@@ -293,11 +295,16 @@ typedef struct {
 
 int mfx_sdpa_bwd(const mfx_sdpa_bwd_args* args, void* stream);
 
-/* Bytes of workspace mfx_sdpa_bwd needs for these arguments. */
+/* Bytes of workspace mfx_sdpa_bwd needs for these arguments: the recomputed
+ * out, lse and delta, and for bf16 / f16 at head size 32 / 96 (D == Dv,
+ * tensors 16-byte aligned with strides a multiple of 8) the copies of q, k,
+ * v, dO, out and the gradients zero-padded to 64 / 128 features that the
+ * matrix-core kernels run on. */
 size_t mfx_sdpa_bwd_workspace_size(const mfx_sdpa_bwd_args* args);
 
 /* Which backward kernels mfx_sdpa_bwd would launch ("mfma_bf16_d128",
- * "generic", ...), or NULL if the arguments are invalid. */
+ * "mfma_bf16_d96" (through the padded copies), "generic", ...), or NULL if
+ * the arguments are invalid. */
 const char* mfx_sdpa_bwd_kernel_name(const mfx_sdpa_bwd_args* args);
 
 /* ==========================================================================
