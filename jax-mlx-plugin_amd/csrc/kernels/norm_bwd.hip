@@ -35,7 +35,7 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
   constexpr int VEC = Vec16<T>::N;
   typedef typename Vec16<T>::type V;
   constexpr int RPB = kBlock / LANES;
-  __shared__ float lds[kBlock / 64];
+  __shared__ float lds[2 * (kBlock / 64)];
   __shared__ float fold[RPB > 1 ? RPB * LANES * NV * VEC : 1];
 
   const int lane = threadIdx.x % LANES;
@@ -109,8 +109,8 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
         ag[i][j] = fmaf(g[i][j], xv[i][j], ag[i][j]);
         ab[i][j] += g[i][j];
       }
-    const float m1 = row_reduce<LANES, false>(s1, lds) * inv_n;
-    const float m2 = row_reduce<LANES, false>(s2, lds) * inv_n;
+    row_reduce_sum2<LANES>(s1, s2, lds);
+    const float m1 = s1 * inv_n, m2 = s2 * inv_n;
     if (!valid) return;
     V* dr = reinterpret_cast<V*>(dx + row * dxs);
 #pragma unroll
@@ -179,8 +179,8 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_rows(
           ag[i][j] = fmaf(g[i][j], xv[i][j], ag[i][j]);
           ab[i][j] += g[i][j];
         }
-      const float m1 = row_reduce<LANES, false>(s1, lds) * inv_n;
-      const float m2 = row_reduce<LANES, false>(s2, lds) * inv_n;
+      row_reduce_sum2<LANES>(s1, s2, lds);
+      const float m1 = s1 * inv_n, m2 = s2 * inv_n;
       V* dr = reinterpret_cast<V*>(dx + row * dxs);
 #pragma unroll
       for (int i = 0; i < NV; ++i) {

@@ -151,5 +151,34 @@ __device__ __forceinline__ float row_reduce(float v, float* lds) {
   }
 }
 
+// Two independent row sums in one pass: for 256-lane rows one LDS exchange
+// (two barriers) instead of two.  Each value is summed in row_reduce's order,
+// so the results are the same bits.  lds holds 2 * (LANES / 64) floats.
+template <int LANES>
+__device__ __forceinline__ void row_reduce_sum2(float& a, float& b, float* lds) {
+  if constexpr (LANES <= 64) {
+    a = group_sum<LANES>(a);
+    b = group_sum<LANES>(b);
+  } else {
+    a = group_sum<64>(a);
+    b = group_sum<64>(b);
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      lds[2 * wid] = a;
+      lds[2 * wid + 1] = b;
+    }
+    __syncthreads();
+    float ra = lds[0], rb = lds[1];
+#pragma unroll
+    for (int i = 1; i < LANES / 64; ++i) {
+      ra += lds[2 * i];
+      rb += lds[2 * i + 1];
+    }
+    __syncthreads();
+    a = ra;
+    b = rb;
+  }
+}
+
 }  // namespace rowvec
 }  // namespace mfx
