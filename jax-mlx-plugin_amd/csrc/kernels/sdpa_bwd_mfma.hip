@@ -237,7 +237,7 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   // Resource extents end with the last element of the group's last row, so
   // rows past Tq read zeros or (inside the span) rows of the next head,
   // which are masked.
-  Loader<D> qload(qp, p.qs[2], 0, wave, lane), gload(gp, p.dos[2], 0, wave, lane);
+  Loader<D> qload(qp, p.qs[2], 0, D, wave, lane), gload(gp, p.dos[2], 0, D, wave, lane);
   qload.nbytes = (int)(((int64_t)(G - 1) * p.qs[1] + (int64_t)(Tq - 1) * p.qs[2] + D) * 2);
   gload.nbytes = (int)(((int64_t)(G - 1) * p.dos[1] + (int64_t)(Tq - 1) * p.dos[2] + D) * 2);
   auto tile_head = [&](int t) { return t / per_head; };
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
   int kv_end = Tk;
   if (CAUSAL) kv_end = min(Tk, min(Tq, (mblk + 1) * kRows));
   const int ntiles = (kv_end + kTile - 1) / kTile;
-  const Loader<D> kload(kp, p.ks[2], Tk, wave, lane), vload(vp, p.vs[2], Tk, wave, lane);
+  const Loader<D> kload(kp, p.ks[2], Tk, D, wave, lane), vload(vp, p.vs[2], Tk, D, wave, lane);
   auto issue = [&](int t, int st) {
     kload.load(t, smem + (2 * st) * TILE, wave);
     vload.load(t, smem + (2 * st + 1) * TILE, wave);

@@ -406,7 +406,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(SdpaParams p) {
 
     const bf16* kp = static_cast<const bf16*>(p.k) + b * p.ks[0] + hk * p.ks[1];
     const bf16* vp = static_cast<const bf16*>(p.v) + b * p.vs[0] + hk * p.vs[1];
-    const Loader kload(kp, p.ks[2], Tk, 0, lane), vload(vp, p.vs[2], Tk, 0, lane);
+    const Loader kload(kp, p.ks[2], Tk, DV, 0, lane), vload(vp, p.vs[2], Tk, DV, 0, lane);
 
     f32x16 o[DV / 32];
 #pragma unroll

@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kNT, D > 128 ? 1 : 2) void flash_bf16_kernel(SdpaPa
   const int co = !p.causal ? (1 << 30) : 0;
   if (CAUSAL) kv_end = min(Tk, min(Tq + co, (mblk + 1) * kBM + co));
   const int ntiles = (kv_end + kBN - 1) / kBN;
-  const TileLoader<D> kload(kp, ks2, Tk, wave, lane), vload(vp, vs2, Tk, wave, lane);
+  const TileLoader<D> kload(kp, ks2, Tk, D, wave, lane), vload(vp, vs2, Tk, D, wave, lane);
   auto issue = [&](int t, bf16* kl, bf16* vl) {
     kload.load(t, kl, wave);
     vload.load(t, vl, wave);

@@ -149,10 +149,14 @@ using tiles::static_for;
 
 // K / V tile loader: rows [t*kBN, t*kBN + kBN) of one (batch, head) into a
 // swizzled LDS tile.  Instruction i of a wavefront covers rows
-// i*STEP + wave*RPI + lane/DCH of the tile.  One buffer resource spans the
-// tensor's Tk rows; the tile, instruction and lane offsets all go into the
-// per-lane offset, which the hardware range-checks, so rows past Tk read as
-// zeros and no address leaves the tensor.
+// i*STEP + wave*RPI + lane/DCH of the tile.  One buffer resource spans this
+// head's elements, from its first row's first feature to its last row's
+// last feature (row_elems = the head size, which is below D when rows load
+// tile-wide); the tile, instruction and lane offsets all go into the
+// per-lane offset, which the hardware range-checks, so rows past Tk and the
+// last row's features past the head read as zeros and no address leaves the
+// tensor (with heads interleaved in a row, the last head's tile-wide last
+// row would otherwise run past the tensor's end).
 template <int D>
 struct Loader {
   static constexpr int DCH = D / 8;
@@ -166,14 +170,14 @@ struct Loader {
   uint32_t voff;
   uint32_t tile_bytes;
   uint32_t step_bytes;
-  __device__ __forceinline__ Loader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
+  __device__ __forceinline__ Loader(const bf16* b, int64_t row_stride, int Tk, int row_elems, int wave, int lane) {
     tile_bytes = (uint32_t)(kBN * row_stride * 2);
     step_bytes = (uint32_t)(STEP * row_stride * 2);
     const int row = wave * RPI + lane / DCH, slot = lane % DCH;
     voff = (uint32_t)(((int64_t)row * row_stride + (slot ^ tile_swz<D>(row)) * 8) * 2);
 #if defined(__HIP_DEVICE_COMPILE__)
-    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(b), (short)0, (int)((int64_t)Tk * row_stride * 2),
-                                             0x00020000);
+    const int64_t extent = Tk > 0 ? ((int64_t)(Tk - 1) * row_stride + row_elems) * 2 : 0;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(b), (short)0, (int)extent, 0x00020000);
 #endif
   }
   __device__ __forceinline__ void load(int t, bf16* lds, int wave) const {
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   // Tile t needs per-element masking (ragged end, causal diagonal).
   auto edge = [&](int t) { return (t + 1) * kBN > Tk || (CAUSAL && t * kBN + kBN - 1 > q0); };
 
-  const Loader<D> kload(kp, p.ks[2], Tk, wave, lane), vload(vp, p.vs[2], Tk, wave, lane);
+  const Loader<D> kload(kp, p.ks[2], Tk, DV, wave, lane), vload(vp, p.vs[2], Tk, DV, wave, lane);
   bf16* const kst[2] = {smem, smem + TILE};
   bf16* const vst[2] = {smem + 2 * TILE, smem + 3 * TILE};
   // Raw mask value of the next tile wavefront 0 converts at the next barrier.

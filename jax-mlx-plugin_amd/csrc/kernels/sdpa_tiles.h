@@ -81,9 +81,12 @@ __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70);
 // RPI = 64 / (D/8).  Instructions NOFF apart start a swizzle period apart, so
 // they share a per-lane source offset and differ by a scalar offset: NOFF
 // VGPRs per operand, and the tile start and the step are scalar offsets.
-// The resources span the Tk rows of this (batch, head): rows past Tk are out
-// of range and read as zeros (callers also mask their scores, so they
-// contribute exactly 0).
+// The resources span this (batch, head)'s elements, from its first row's
+// first feature to its last row's `row_elems`-th (the head size, below D
+// when rows load tile-wide): rows past Tk and the last row's features past
+// the head are out of range and read as zeros (callers also mask their
+// scores, so they contribute exactly 0), and no address leaves the tensor,
+// also when heads are interleaved within a row.
 template <int D, int BN, int NW>
 struct TileLoader {
   static constexpr int DCH = D / 8;
@@ -98,15 +101,16 @@ struct TileLoader {
     return true;
   }
   bf16* base;
-  int nbytes;             // extent of the resource: Tk rows
+  int nbytes;             // extent of the resource: to the last row's last element
   uint32_t voff[NOFF];    // per-lane source offsets of instructions 0 .. NOFF-1
   uint32_t period_bytes;  // scalar offset step per NOFF instructions
   uint32_t tile_bytes;    // scalar offset step per tile
 
-  __device__ __forceinline__ TileLoader(const bf16* b, int64_t row_stride, int Tk, int wave, int lane) {
+  __device__ __forceinline__ TileLoader(const bf16* b, int64_t row_stride, int Tk, int row_elems, int wave,
+                                        int lane) {
     static_assert(swz_period_divides(NOFF * STEP), "the swizzle must repeat every NOFF instructions");
     base = const_cast<bf16*>(b);
-    nbytes = (int)((int64_t)Tk * row_stride * 2);
+    nbytes = Tk > 0 ? (int)(((int64_t)(Tk - 1) * row_stride + row_elems) * 2) : 0;
     tile_bytes = (uint32_t)(BN * row_stride * 2);
     period_bytes = (uint32_t)(NOFF * STEP * row_stride * 2);
 #pragma unroll
