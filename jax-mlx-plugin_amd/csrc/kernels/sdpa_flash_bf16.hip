@@ -342,11 +342,11 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 bool flash_bf16_supports(const SdpaParams& p) {
   if (p.dtype != MFX_BF16 && p.dtype != MFX_F16) return false;
   if (!(p.scale_log2 > 0.f)) return false;  // the exp2 FMA folds a positive scale
-  // K/V rows are read through one buffer resource per head spanning its Tk
-  // rows, range-checked on 31-bit lane offsets: row strides of at least D
-  // (rows past Tk then start at or past the extent and read as zeros; a
-  // smaller stride, such as 0 for a broadcast view, would leave rows past Tk
-  // inside it and the last row's tail outside).
+  // K/V rows are read through one buffer resource per head ending at its
+  // last row's last feature, range-checked on 31-bit lane offsets: row
+  // strides of at least D (rows past Tk then start at or past the extent and
+  // read as zeros; a smaller stride, such as 0 for a broadcast view, would
+  // leave rows past Tk inside it).
   if (p.ks[2] < p.D || p.vs[2] < p.Dv) return false;
   if ((int64_t)p.Tk * p.ks[2] * 2 >= (1LL << 31) || (int64_t)p.Tk * p.vs[2] * 2 >= (1LL << 31)) return false;
   if (p.D != p.Dv || (p.D != 32 && p.D != 64 && p.D != 96 && p.D != 128 && p.D != 256)) return false;
@@ -355,8 +355,7 @@ bool flash_bf16_supports(const SdpaParams& p) {
   if (p.mask && p.ms[2] != 0 && p.Tq > 1 && p.D != 64 && p.D != 128 && p.D != 256) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   for (int i = 0; i < 3; ++i)
-    if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.os[i] % 4) return false;
-  if (p.os[2] % 4) return false;
+    if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.os[i] % 8) return false;  // 16-byte rows
   return true;
 }
 
