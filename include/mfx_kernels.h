@@ -253,7 +253,7 @@ const char* mfx_sdpa_kernel_name(const mfx_sdpa_args* args);
  * fwd_out_strides) and fwd_lse (that call's lse output), both or neither;
  * with both, the recompute is skipped.  The gradients then equal the
  * recomputing call's bit for bit whenever the forward ran the kernel the
- * recompute runs (out 16-byte aligned with strides a multiple of 4 -- every
+ * recompute runs (out 16-byte aligned with strides a multiple of 8 -- every
  * output the plugin's planner allocates).  A plan that
  * runs a forward and its backward passes them along; the reference's
  * custom_call @mlx_sdpa_bwd interface (q, k, v, grad_out) has no slot for
