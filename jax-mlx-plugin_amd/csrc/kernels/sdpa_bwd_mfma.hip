@@ -133,10 +133,19 @@ __device__ __forceinline__ void load_frags(const bf16* base, int64_t stride, int
   }
 }
 
-// Stores a transposed accumulator (rows d, lane column = one output row) as
-// bf16, 4 features per store, times `mul`.
+// Stores this wavefront's 32 output rows (lane column l32 = row, features
+// dt*32 + g*8 + half*4 + e of a transposed accumulator, times `mul`) as
+// whole rows: written into the wavefront's 32 x D region of free LDS
+// (16-byte chunk c of row r at slot c ^ (r % (D/8)), so neither the 8-byte
+// writes nor the 16-byte reads meet more than two lanes on a bank), read
+// back row-contiguous, 16 bytes per lane, so each store instruction writes
+// 64 / (D/8) whole rows.  Row r goes to dst + r * stride when r < nvalid
+// (rows 16-byte aligned, checked on the host).
 template <int D, int E>
-__device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int half, float mul) {
+__device__ __forceinline__ void store_rows_lds(bf16* lds, bf16* dst, int64_t stride, int nvalid, const f32x16* acc,
+                                               int l32, int half, int lane, float mul) {
+  constexpr int CPR = D / 8;    // 16-byte chunks per row
+  constexpr int RPS = 64 / CPR;  // rows per store instruction
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -144,8 +153,15 @@ __device__ __forceinline__ void store_rowT(bf16* row, const f32x16* acc, int hal
       u16x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) w[e] = store_e<E>(acc[dt][g * 4 + e] * mul);
-      *reinterpret_cast<u16x4*>(row + dt * 32 + g * 8 + half * 4) = w;
+      const int c = dt * 4 + g;
+      *reinterpret_cast<u16x4*>(lds + l32 * D + (c ^ (l32 & (CPR - 1))) * 8 + half * 4) = w;
     }
+#pragma unroll
+  for (int k = 0; k < 32 / RPS; ++k) {
+    const int r = k * RPS + lane / CPR, c = lane % CPR;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * D + (c ^ (r & (CPR - 1))) * 8);
+    if (r < nvalid) *reinterpret_cast<u32x4*>(dst + r * stride + c * 8) = v;
+  }
 }
 
 // ----------------------------------------------------------------- dK, dV
@@ -478,11 +494,20 @@ __global__ __launch_bounds__(kNT, 1) void bwd_dkdv_mfma(SdpaBwdParams p) {
   }
 
   PHASE(fence(); ph_slot(kPhCEpi) = ph_now(); fence();)
-  if (key < Tk) {
-    bf16* dko = static_cast<bf16*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + (int64_t)key * p.dks[2];
-    bf16* dvo = static_cast<bf16*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + (int64_t)key * p.dvs[2];
-    store_rowT<D, E>(dko, dk, half, p.scale);
-    store_rowT<D, E>(dvo, dv, half, 1.f);
+  // Every wavefront's last Y has read its Q / dO stage: the stages take the
+  // dK and dV rows on their way out.  (The first key comes from an opaque
+  // copy here, so no address is hoisted into the loop.)
+  __syncthreads();
+  {
+    int k0 = kw;
+    asm volatile("" : "+v"(k0));
+    const int nvalid = min(max(Tk - k0, 0), 32);
+    bf16* const st = reinterpret_cast<bf16*>(smem) + wave * 2 * 32 * D;
+    store_rows_lds<D, E>(st, static_cast<bf16*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + (int64_t)k0 * p.dks[2],
+                         p.dks[2], nvalid, dk, l32, half, lane, p.scale);
+    store_rows_lds<D, E>(st + 32 * D,
+                         static_cast<bf16*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + (int64_t)k0 * p.dvs[2],
+                         p.dvs[2], nvalid, dv, l32, half, lane, 1.f);
   }
 #if defined(MFX_PHASE_TIMERS)
   {
@@ -751,9 +776,16 @@ __global__ __launch_bounds__(kNT, 2) void bwd_dq_mfma(SdpaBwdParams p) {
     __syncthreads();
   }
 
-  if (qi < Tq) {
-    bf16* dqo = static_cast<bf16*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + (int64_t)qi * p.dqs[2];
-    store_rowT<D, E>(dqo, dq, half, p.scale);
+  // Every step ended at a barrier after its reads and with no load in
+  // flight: the stages take the dQ rows on their way out.  (The first row
+  // comes from an opaque copy here, so no address is hoisted into the loop.)
+  {
+    int r0 = q0;
+    asm volatile("" : "+v"(r0));
+    const int nvalid = min(max(Tq - r0, 0), 32);
+    store_rows_lds<D, E>(smem + wave * 32 * D,
+                         static_cast<bf16*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + (int64_t)r0 * p.dqs[2], p.dqs[2],
+                         nvalid, dq, l32, half, lane, p.scale);
   }
 }
 
@@ -788,8 +820,8 @@ bool bwd_mfma_supports(const SdpaBwdParams& p) {
   for (const void* ptr : ptrs)
     if (!aligned16(ptr)) return false;
   for (int i = 0; i < 3; ++i)
-    if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.dos[i] % 8 || p.dqs[i] % 4 || p.dks[i] % 4 ||
-        p.dvs[i] % 4 || p.os[i] % 8)
+    if (p.qs[i] % 8 || p.ks[i] % 8 || p.vs[i] % 8 || p.dos[i] % 8 || p.dqs[i] % 8 || p.dks[i] % 8 ||
+        p.dvs[i] % 8 || p.os[i] % 8)
       return false;
   // K / V / Q / dO rows are read through buffer resources whose extents
   // assume rows of at least D elements (rows past the end then read zeros).
