@@ -133,37 +133,6 @@ __device__ __forceinline__ void load_frags(const bf16* base, int64_t stride, int
   }
 }
 
-// Stores this wavefront's 32 output rows (lane column l32 = row, features
-// dt*32 + g*8 + half*4 + e of a transposed accumulator, times `mul`) as
-// whole rows: written into the wavefront's 32 x D region of free LDS
-// (16-byte chunk c of row r at slot c ^ (r % (D/8)), so neither the 8-byte
-// writes nor the 16-byte reads meet more than two lanes on a bank), read
-// back row-contiguous, 16 bytes per lane, so each store instruction writes
-// 64 / (D/8) whole rows.  Row r goes to dst + r * stride when r < nvalid
-// (rows 16-byte aligned, checked on the host).
-template <int D, int E>
-__device__ __forceinline__ void store_rows_lds(bf16* lds, bf16* dst, int64_t stride, int nvalid, const f32x16* acc,
-                                               int l32, int half, int lane, float mul) {
-  constexpr int CPR = D / 8;    // 16-byte chunks per row
-  constexpr int RPS = 64 / CPR;  // rows per store instruction
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u16x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = store_e<E>(acc[dt][g * 4 + e] * mul);
-      const int c = dt * 4 + g;
-      *reinterpret_cast<u16x4*>(lds + l32 * D + (c ^ (l32 & (CPR - 1))) * 8 + half * 4) = w;
-    }
-#pragma unroll
-  for (int k = 0; k < 32 / RPS; ++k) {
-    const int r = k * RPS + lane / CPR, c = lane % CPR;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * D + (c ^ (r & (CPR - 1))) * 8);
-    if (r < nvalid) *reinterpret_cast<u32x4*>(dst + r * stride + c * 8) = v;
-  }
-}
-
 // ----------------------------------------------------------------- dK, dV
 
 // dK / dV run one wavefront per SIMD at d = 128 (the 32 keys' K and V
