@@ -327,6 +327,44 @@ __global__ __launch_bounds__(kNT, 2) void gemm16_kernel(Params p) {
   // Lane: row m = m0 + wm*64 + i*32 + l32; accumulator element g*4 + e:
   // column n = n0 + wn*64 + j*32 + g*8 + half*4 + e (N % 4 == 0: a run of
   // 4 is all in range or all out).
+  if constexpr (OT != 0) {
+    // 16-bit outputs through LDS, so each store instruction writes 8 rows x
+    // 128 bytes of the wavefront's 64 x 64 block instead of 32 rows x 16:
+    // after a barrier the stages are free (every wavefront's last fragments
+    // are read and no load is in flight), 8 KB per wavefront; 16-byte chunk
+    // c of row r at slot c ^ (r % 8).  Needs whole 16-byte chunks in range
+    // and aligned: N, ldc and the batch stride multiples of 8, C 16-byte
+    // aligned (uniform over the grid).
+    if (!p.part && ((N | p.ldc) & 7) == 0 && (p.sc & 7) == 0 && ((uintptr_t)p.c & 15) == 0) {
+      __syncthreads();
+      bf16* const st = smem + wave * 64 * 64;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            u16x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = store_e<OT - 1>(acc[j][i][g * 4 + e]);
+            const int r = i * 32 + l32, c = j * 4 + g;
+            *reinterpret_cast<u16x4*>(st + r * 64 + (c ^ (r & 7)) * 8 + half * 4) = w;
+          }
+      // (The block's first row comes from an opaque copy, so no address is
+      // hoisted into the k loop.)
+      int mb = m0 + wm * 64;
+      asm volatile("" : "+v"(mb));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int r = k * 8 + (lane >> 3), c = lane & 7;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * 64 + (c ^ (r & 7)) * 8);
+        const int m = mb + r, n = n0 + wn * 64 + c * 8;
+        if (m < M && n < N)
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.c) + bz * p.sc + (int64_t)m * p.ldc + n) = v;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int m = m0 + wm * 64 + i * 32 + l32;
