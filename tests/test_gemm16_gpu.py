@@ -9,6 +9,8 @@ u = 0 for f32 outputs, 2^-8 for bf16 and 2^-11 for f16 (unit roundoff), ref
 the fp64 product of the 16-bit inputs.  A dropped, doubled or misplaced
 k-term (a k slot order that differs between the operands, a wrong swizzle,
 a transposed fragment) misses it by orders of magnitude."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -119,6 +121,37 @@ def test_gemm16_reads_nothing_past_its_operands(torch, nt, ta, tb, m, n, k):
     a = fa[: m * k].view((k, m) if ta else (m, k))
     b = fb[: k * n].view((n, k) if tb else (k, n))
     _check(torch, nt, a, b, ta, tb, "f32", "gemm_bf16_tile")
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_gemm16_16bit_outputs_in_8_byte_pieces(torch, nt, ta, dt):
+    """16-bit outputs whose rows are not whole 16-byte chunks take the
+    8-byte stores instead of the rows staged through LDS: N % 8 == 4 (B
+    transposed, so its rows stay aligned), and an output view 8 bytes past
+    a 16-byte boundary with a leading dim of 4 mod 8.  Both against fp64, and
+    the view's neighbours untouched."""
+    g = torch.Generator(device="cpu").manual_seed(41 + ta)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16}[dt]
+    a, b = _operands(torch, g, 136, 100, 64, ta, True, torch.bfloat16)
+    _check(torch, nt, a, b, ta, True, dt, "gemm_bf16_tile")
+    a, b = _operands(torch, g, 136, 96, 64, ta, False, torch.bfloat16)
+    buf = torch.full((136, 108), 7.0, dtype=tdt, device="cuda")
+    out = buf[:, 4:100]  # ldc 108, first element 8 bytes past the row start
+    assert out.data_ptr() % 16 == 8 and out.stride(0) % 8 == 4
+    # (the Python wrapper writes contiguous outputs: the view's leading dim
+    # goes in through the C ABI's ldc)
+    args = nt.gemm_args(a, b, out, ta, False)
+    args.ldc = out.stride(0)
+    assert nt.load().mfx_gemm_kernel_name(ctypes.byref(args)).decode() == "gemm_bf16_tile"
+    nt.check(nt.load().mfx_gemm(ctypes.byref(args), nt._stream_handle(a)))
+    torch.cuda.synchronize()
+    a64, b64 = _op(a.double().cpu().numpy(), ta), b.double().cpu().numpy()
+    ref = a64 @ b64
+    bound = np.abs(a64) @ np.abs(b64) * 66 * 2.0 ** -23 + U_OUT[dt] * np.abs(ref) + 1e-30
+    assert (np.abs(out.double().cpu().numpy() - ref) <= bound).all()
+    rest = buf.double().cpu().numpy()
+    assert (rest[:, :4] == 7.0).all() and (rest[:, 100:] == 7.0).all()
 
 
 def test_gemm16_outside_tile_rules_goes_to_rocblas(torch, nt):
