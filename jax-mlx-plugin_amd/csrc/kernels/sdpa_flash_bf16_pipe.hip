@@ -680,7 +680,9 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
     for (int k = 0; k < 32 / RPS; ++k) {
       const int r = k * RPS + lane / CPR, c = lane % CPR;
       const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * DV + (c ^ (r & (CPR - 1))) * 8);
-      if (q0 + r < Tq) *reinterpret_cast<u32x4*>(op + (int64_t)(q0 + r) * os2 + c * 8) = v;
+      // Whole lines, written once: streamed past the L2 (so the kernel's
+      // end has no output lines to write back).
+      if (q0 + r < Tq) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(op + (int64_t)(q0 + r) * os2 + c * 8));
     }
   } else if constexpr (MT == 0) {
     // Head sizes 32 and 96 (rows of 64 / 192 bytes): lanes l32 and l32 + 32 trade one 4-feature group of each pair (g, g+1)
