@@ -334,7 +334,8 @@ __global__ __launch_bounds__(kNT, 2) void gemm16_kernel(Params p) {
     // are read and no load is in flight), 8 KB per wavefront; 16-byte chunk
     // c of row r at slot c ^ (r % 8).  Needs whole 16-byte chunks in range
     // and aligned: N, ldc and the batch stride multiples of 8, C 16-byte
-    // aligned (uniform over the grid).
+    // aligned (uniform over the grid).  The rows are streamed past the L2
+    // (whole lines, written once).
     if (!p.part && ((N | p.ldc) & 7) == 0 && (p.sc & 7) == 0 && ((uintptr_t)p.c & 15) == 0) {
       __syncthreads();
       bf16* const st = smem + wave * 64 * 64;
@@ -360,7 +361,8 @@ __global__ __launch_bounds__(kNT, 2) void gemm16_kernel(Params p) {
         const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * 64 + (c ^ (r & 7)) * 8);
         const int m = mb + r, n = n0 + wn * 64 + c * 8;
         if (m < M && n < N)
-          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.c) + bz * p.sc + (int64_t)m * p.ldc + n) = v;
+          __builtin_nontemporal_store(
+              v, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.c) + bz * p.sc + (int64_t)m * p.ldc + n));
       }
       return;
     }

@@ -122,8 +122,9 @@ constexpr float kMaxP = E == 0 ? 65536.f : 32768.f;
 // (16-byte chunk c of row r at slot c ^ (r % (D/8)), so neither the 8-byte
 // writes nor the 16-byte reads meet more than two lanes on a bank), read
 // back row-contiguous, 16 bytes per lane, so each store instruction writes
-// 64 / (D/8) whole rows.  Row r goes to dst + r * stride when r < nvalid
-// (rows 16-byte aligned, checked on the host).
+// 64 / (D/8) whole rows, streamed past the L2 (whole lines, written once).
+// Row r goes to dst + r * stride when r < nvalid (rows 16-byte aligned,
+// checked on the host).
 template <int D, int E>
 __device__ __forceinline__ void store_rows_lds(bf16* lds, bf16* dst, int64_t stride, int nvalid, const f32x16* acc,
                                                int l32, int half, int lane, float mul) {
@@ -143,7 +144,7 @@ __device__ __forceinline__ void store_rows_lds(bf16* lds, bf16* dst, int64_t str
   for (int k = 0; k < 32 / RPS; ++k) {
     const int r = k * RPS + lane / CPR, c = lane % CPR;
     const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * D + (c ^ (r & (CPR - 1))) * 8);
-    if (r < nvalid) *reinterpret_cast<u32x4*>(dst + r * stride + c * 8) = v;
+    if (r < nvalid) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + r * stride + c * 8));
   }
 }
 
