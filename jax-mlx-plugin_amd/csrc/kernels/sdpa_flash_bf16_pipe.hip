@@ -654,16 +654,18 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
   int qo = qi;
   asm volatile("" : "+v"(qo));
   fence();
-  if constexpr (DV == 128 || DV == 64) {
+  {
     // Through LDS, so each store instruction writes whole rows: the K stages
     // are free (after the last barrier no wavefront reads them -- a last
     // tile reads V only, mask rows have an array of their own -- and no DMA
     // writes them), 32 rows x DV per wavefront.  16-byte chunk c of row r
-    // sits at slot c ^ (r % CPR), so neither the 8-byte writes nor the
-    // row-contiguous 16-byte reads meet more than two lanes on a bank.
-    // Output rows are 16-byte aligned (checked on the host).
-    constexpr int CPR = DV / 8;    // 16-byte chunks per row
-    constexpr int RPS = 64 / CPR;  // rows per store instruction
+    // sits at slot c ^ (r & SWZ), a permutation within each group of SWZ + 1
+    // chunks (so 12-chunk rows, head size 96, stay inside the row), which
+    // keeps the 8-byte writes and the row-contiguous 16-byte reads to a few
+    // lanes per bank.  Output rows are 16-byte aligned (checked on the host).
+    constexpr int CPR = DV / 8;    // 16-byte chunks per row: 4, 8, 12, 16
+    constexpr int RPS = 64 / CPR;  // whole rows per store instruction
+    constexpr int SWZ = CPR % 16 == 0 ? 15 : CPR % 8 == 0 ? 7 : 3;
     bf16* const st = smem + wave * 32 * DV;
     const int r0 = qo - q0;  // = l32
 #pragma unroll
@@ -674,53 +676,19 @@ __global__ __launch_bounds__(kNT, 2) void flash_bf16_pipe_kernel(SdpaParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[e] = store_e<E>(o[dt][g * 4 + e] * inv);
         const int c = dt * 4 + g;
-        *reinterpret_cast<u16x4*>(st + r0 * DV + (c ^ (r0 & (CPR - 1))) * 8 + half * 4) = w;
+        *reinterpret_cast<u16x4*>(st + r0 * DV + (c ^ (r0 & SWZ)) * 8 + half * 4) = w;
       }
 #pragma unroll
-    for (int k = 0; k < 32 / RPS; ++k) {
+    for (int k = 0; k < (32 + RPS - 1) / RPS; ++k) {
       const int r = k * RPS + lane / CPR, c = lane % CPR;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * DV + (c ^ (r & (CPR - 1))) * 8);
-      // Whole lines, written once: streamed past the L2 (so the kernel's
-      // end has no output lines to write back).
-      if (q0 + r < Tq) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(op + (int64_t)(q0 + r) * os2 + c * 8));
+      if (lane < RPS * CPR && r < 32) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * DV + (c ^ (r & SWZ)) * 8);
+        // Whole lines, written once: streamed past the L2 (so the kernel's
+        // end has no output lines to write back).
+        if (q0 + r < Tq)
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(op + (int64_t)(q0 + r) * os2 + c * 8));
+      }
     }
-  } else if constexpr (MT == 0) {
-    // Head sizes 32 and 96 (rows of 64 / 192 bytes): lanes l32 and l32 + 32 trade one 4-feature group of each pair (g, g+1)
-    // (v_permlane32_swap), so each lane stores 8 consecutive features, 16
-    // bytes: half 0 group g, half 1 group g+1.
-    bf16* orow = op + (int64_t)min(qo, Tq - 1) * os2;
-#pragma unroll
-    for (int dt = 0; dt < DV / 32; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; g += 2) {
-        u16x4 wa, wb;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wa[e] = store_e<E>(o[dt][g * 4 + e] * inv);
-          wb[e] = store_e<E>(o[dt][(g + 1) * 4 + e] * inv);
-        }
-        const u32x2 ua = __builtin_bit_cast(u32x2, wa), ub = __builtin_bit_cast(u32x2, wb);
-        // half 0 sends group g+1, half 1 group g; each receives the other's
-        const u32x2 snd = half ? ua : ub;
-        const auto s0 = __builtin_amdgcn_permlane32_swap(snd.x, snd.x, false, false);
-        const auto s1 = __builtin_amdgcn_permlane32_swap(snd.y, snd.y, false, false);
-        const uint32_t r0 = half ? s0[0] : s0[1], r1 = half ? s1[0] : s1[1];
-        const u32x4 out = half ? u32x4{r0, r1, ub.x, ub.y} : u32x4{ua.x, ua.y, r0, r1};
-        if (qo < Tq) *reinterpret_cast<u32x4*>(orow + dt * 32 + (g + half) * 8) = out;
-      }
-  } else if (qo < Tq) {
-    // Head sizes 32 and 96 with a mask: 8-byte pieces (those forms have no
-    // registers to spare for the exchange).
-    bf16* orow = op + (int64_t)qo * os2;
-#pragma unroll
-    for (int dt = 0; dt < DV / 32; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u16x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = store_e<E>(o[dt][g * 4 + e] * inv);
-        *reinterpret_cast<u16x4*>(orow + dt * 32 + g * 8 + half * 4) = w;
-      }
   }
   PHASE(fence(); ph.write(lane, id * kNW + wave, bh, mblk, N, nw, c_epi);)
 }
