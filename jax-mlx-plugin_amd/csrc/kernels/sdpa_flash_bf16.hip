@@ -300,7 +300,18 @@ __global__ __launch_bounds__(kNT, D > 128 ? 1 : 2) void flash_bf16_kernel(SdpaPa
   const float lt = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / lt;
   if (p.lse && half == 0 && qi < Tq) p.lse[(int64_t)bh * Tq + qi] = b_run + __log2f(lt);
-  if (qi < Tq) {
+  if constexpr (D <= 128) {
+    // Every iteration ended at a barrier after its reads and with no load in
+    // flight: the tile arrays take the output rows on their way out (k0
+    // holds wavefronts 0 and 1, v0 wavefronts 2 and 3), stored as whole
+    // rows streamed past the L2.  (The first row comes from an opaque copy,
+    // so no address is hoisted into the loop.)  At D = 256, one workgroup per
+    // CU, nothing would cover the LDS round trip: 8-byte pieces there.
+    int r0 = q0;
+    asm volatile("" : "+v"(r0));
+    store_rows_lds<D, E>((wave < 2 ? k0 : v0) + (wave & 1) * 32 * D, op + (int64_t)r0 * os2, os2,
+                         min(max(Tq - r0, 0), 32), o, l32, half, lane, inv);
+  } else if (qi < Tq) {
     bf16* orow = op + qi * os2;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
